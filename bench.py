@@ -1,0 +1,225 @@
+"""LeanSelect prefill hot path benchmark on one MI355X.
+
+One step = one MiniCPM4.1-8B attention layer of LeanSelect sparse prefill on a
+128K-token sequence (bf16, 32 query / 2 KV heads, head_dim 128, page 64,
+budget 64 pages = 1 sink + 4 local + 59 selected): compressed keys, page
+selection and block-sparse attention, with inputs resident in HBM.
+
+Prints one JSON line (metric: ms per layer, lower is better) with a roofline
+object for the dominant kernel (block-sparse attention) measured with HIP
+events on the launch stream, per-stage timings, and the CPU oracle timed on a
+bounded row sample of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from leanselect_amd import workloads  # noqa: E402
+from leanselect_amd.ops import compress_k, leanselect_prefill_topk_idx, sparse_attention  # noqa: E402
+
+WORKLOADS = {
+    "minicpm41_8b_layer_128k": dict(seq_lens=(131072,)),
+    "minicpm41_8b_layer_32k": dict(seq_lens=(32768,)),
+    "minicpm41_8b_layer_ragged_8k_24k_48k_96k": dict(seq_lens=(8192, 24576, 49152, 98304)),
+}
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def attention_keys(ids: torch.Tensor, cu_host: list[int]) -> int:
+    """Sum over (group, row) of the keys the row attends (causal, each page once)."""
+    G, N, T = ids.shape
+    dev = ids.device
+    t_rel = torch.empty(N, dtype=torch.long, device=dev)
+    lk = torch.empty(N, dtype=torch.long, device=dev)
+    for b in range(len(cu_host) - 1):
+        s, e = cu_host[b], cu_host[b + 1]
+        t_rel[s:e] = torch.arange(e - s, device=dev)
+        lk[s:e] = e - s
+    jmax = torch.minimum(t_rel, lk - 1)  # prefill: len_q == len_k
+    p = ids.long()
+    valid = p >= 0
+    keys = torch.clamp(jmax[None, :, None] - 64 * p + 1, min=0, max=64)
+    return int((keys * valid).sum())
+
+
+def selection_flops(case, D: int = 128, F: int = 128) -> float:
+    """q~ projection + k~ projection + the atom dots of the non-forced visible pages."""
+    H, G = case.q.shape[1], case.k.shape[1]
+    N = case.cu_host[-1]
+    total = 2.0 * N * G * (H // G) * D * F
+    atom_dots = 0
+    for b in range(len(case.cu_host) - 1):
+        n = case.cu_host[b + 1] - case.cu_host[b]
+        A = (n - 32) // 16 + 1 if n >= 32 else 0
+        total += 2.0 * A * G * D * F
+        for qb in range((n + 63) // 64):
+            hi = min(4 * (qb - case.local_blocks) - 1, A - 1)  # last atom of page qb-local-1
+            lo = max(4 * case.init_blocks - 1, 0)
+            rows = min(64, n - 64 * qb)
+            atom_dots += rows * max(0, hi - lo + 1)
+    return total + 2.0 * G * F * atom_dots
+
+
+def _event_ms(fn, iters: int) -> float:
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def cpu_baseline(case, rows_per_seq: int, threads: int) -> dict:
+    """The CPU oracle on a row sample, scaled to ms per layer."""
+    import oracle
+
+    torch.set_num_threads(threads)
+    q, k, v = case.q.cpu(), case.k.cpu(), case.v.cpu()
+    cu = case.cu_host
+    rows = []
+    for b in range(len(cu) - 1):
+        n = cu[b + 1] - cu[b]
+        step = max(1, n // rows_per_seq)
+        rows += list(range(cu[b] + step - 1, cu[b + 1], step))
+    sel = case.selector
+    t0 = time.perf_counter()
+    kc, cu_c = oracle.compress_k(k, cu)
+    qf, kf = oracle.fused_weights(sel.head_mix.cpu(), sel.kv_head_mix.cpu(), sel.q_proj.cpu(),
+                                  sel.k_proj.cpu(), q.dtype)
+    t1 = time.perf_counter()
+    ids = oracle.select_prefill(q, kc, cu, cu_c.tolist(), qf, kf, topk=case.topk,
+                                init_blocks=case.init_blocks, local_blocks=case.local_blocks,
+                                rows=rows)
+    t2 = time.perf_counter()
+    oracle.sparse_attention(q, k, v, cu, cu, ids, rows=rows, ids_rows_aligned=True)
+    t3 = time.perf_counter()
+    N = cu[-1]
+    scale = N / len(rows)
+    ms = 1e3 * ((t1 - t0) + (t2 - t1) * scale + (t3 - t2) * scale)
+    return {
+        "value": round(ms, 1),
+        "unit": "ms/layer",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"CPU oracle (float64 torch restatement) on {len(rows)} of {N} query rows "
+                   f"spread evenly per sequence: compressed keys in full ({1e3*(t1-t0):.0f} ms), "
+                   f"selection {1e3*(t2-t1):.0f} ms and attention {1e3*(t3-t2):.0f} ms for the "
+                   f"sample, both scaled by {scale:.1f}"),
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="minicpm41_8b_layer_128k", choices=sorted(WORKLOADS))
+    ap.add_argument("--kernel-iters", type=int, default=5)
+    ap.add_argument("--cpu-rows-per-seq", type=int, default=256)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this path runs on a single device "
+              f"(--gpus {args.gpus} is not supported)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = WORKLOADS[args.workload]
+    print(f"[bench] generating {args.workload} ...", file=sys.stderr, flush=True)
+    case = workloads.hidden_space_layer(wl["seq_lens"], device=dev, seed=0)
+    cu, cu_host = case.cu_seqlens, case.cu_host
+    max_len = case.max_seqlen
+    kw = dict(topk=case.topk, init_blocks=case.init_blocks, local_blocks=case.local_blocks,
+              cu_seqlens_q_host=cu_host)
+
+    def step():
+        kc, cu_c = compress_k(case.k, cu, cu_seqlens_host=cu_host)
+        ids = leanselect_prefill_topk_idx(case.q, kc, cu, cu_c, case.selector, **kw)
+        return sparse_attention(case.q, case.k, case.v, cu, cu, max_len, max_len, ids), ids
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    print(f"[bench] warmup done, timing {args.steps} steps", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out, ids = step()
+    torch.cuda.synchronize()
+    ms_step = 1e3 * (time.perf_counter() - t0) / args.steps
+
+    # Per-stage kernel time with HIP events on the launch stream.
+    kc, cu_c = compress_k(case.k, cu, cu_seqlens_host=cu_host)
+    it = args.kernel_iters
+    ms_compress = _event_ms(lambda: compress_k(case.k, cu, cu_seqlens_host=cu_host), it)
+    ms_select = _event_ms(lambda: leanselect_prefill_topk_idx(case.q, kc, cu, cu_c, case.selector, **kw), it)
+    ms_attn = _event_ms(lambda: sparse_attention(case.q, case.k, case.v, cu, cu, max_len, max_len, ids), it)
+
+    H, G, D = case.q.shape[1], case.k.shape[1], case.q.shape[2]
+    n_keys = attention_keys(ids, cu_host)
+    attn_flops = 4.0 * (H // G) * D * n_keys
+    sel_flops = selection_flops(case)
+    attn_tflops = attn_flops / (ms_attn * 1e-3) / 1e12
+    N = cu_host[-1]
+    result = {
+        "metric": "selector+sparse-attn prefill ms/layer @128K",
+        "value": round(ms_step, 3),
+        "unit": "ms/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded hidden states with planted rank-8 page topics, random-init projections)",
+        "config": {
+            "workload": args.workload,
+            "seq_lens": list(wl["seq_lens"]),
+            "heads_q": H, "heads_kv": G, "head_dim": D, "page": 64,
+            "budget_pages": case.topk, "sink_pages": case.init_blocks,
+            "local_blocks": case.local_blocks, "router": "4x32",
+            "parallelism": "single-gpu",
+        },
+        "stages_ms": {"compress_k": round(ms_compress, 4), "select": round(ms_select, 4),
+                      "sparse_attention": round(ms_attn, 4)},
+        "roofline": {
+            "kernel": "ls_attn_kernel (block-sparse attention op incl. V staging)",
+            "bound": "mfma",
+            "achieved": round(attn_tflops, 2),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "algorithmic_flops": attn_flops,
+            "avg_keys_per_row": round(n_keys / (G * N), 1),
+        },
+        "secondary": {
+            "select_tflops": round(sel_flops / (ms_select * 1e-3) / 1e12, 2),
+            "select_flops": sel_flops,
+        },
+    }
+    if not args.no_cpu_baseline:
+        threads = len(os.sched_getaffinity(0))
+        print(f"[bench] CPU baseline on {threads} threads ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(case, args.cpu_rows_per_seq, threads)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

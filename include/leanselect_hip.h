@@ -1,0 +1,201 @@
+/*
+ * leanselect_hip.h -- C ABI of the MI355X (gfx950) LeanSelect prefill hot path.
+ *
+ * Plain pointers and sizes only.  Every tensor argument is a device pointer to
+ * caller-owned memory; `cu_seqlens*` arrays are int32 device arrays of
+ * `batch + 1` prefix offsets.  `stream` is a hipStream_t passed as void*.
+ * Each entry point enqueues its work on `stream` and returns without
+ * synchronising.  The return value is LS_OK or an LS_ERR_* code;
+ * ls_last_error() then describes the failure (thread-local).
+ *
+ * Element types (argument `dtype`): LS_F32, LS_BF16, LS_F16.
+ *
+ * Paths in comments are relative to the LeanSelect repository root;
+ * "paper1.patch:N" is line N of third_party/infllmv2/paper1.patch.
+ */
+#ifndef LEANSELECT_HIP_H
+#define LEANSELECT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { LS_F32 = 0, LS_BF16 = 1, LS_F16 = 2 };
+
+enum {
+  LS_OK = 0,
+  LS_ERR_INVALID = 1,     /* bad shape, geometry or pointer */
+  LS_ERR_UNSUPPORTED = 2, /* valid request outside what the kernels support */
+  LS_ERR_WORKSPACE = 3,   /* workspace missing or too small */
+  LS_ERR_HIP = 4          /* a HIP runtime call failed */
+};
+
+/* Library version (major*10000 + minor*100 + patch). */
+int ls_version(void);
+
+/* Message for the last failing call on this host thread. */
+const char* ls_last_error(void);
+
+/*
+ * Compressed keys: mean of `kernel_size`-token windows at `kernel_stride`,
+ * per sequence (windows never cross a sequence boundary; a sequence shorter
+ * than `kernel_size` yields no window).
+ *   k        [total_k, num_kv_heads, head_dim], rows `k_row_stride` elements apart
+ *   out      [total_atoms, num_kv_heads, head_dim] contiguous, same dtype
+ *   cu_out   int32 [batch + 1] compressed prefix offsets (written)
+ * `total_atoms` must equal sum_b max(0, (len_b - kernel_size) / kernel_stride + 1).
+ * Replaces CompressK.forward + calc_chunks_with_stride
+ * (leanselect/models/minicpm.py:1158-1185, 711-750).
+ */
+int ls_compress_k_varlen(const void* k, int64_t k_row_stride, const int32_t* cu_seqlens_k,
+                         int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                         int32_t kernel_size, int32_t kernel_stride, void* out,
+                         int64_t total_atoms, int32_t* cu_out, void* stream);
+
+/*
+ * Folded router weights in the reference layout:
+ *   q_fused[h, d, r*F + j]  = head_mix[h, r]    * q_proj[r, d, j]   ([H, D, R*F])
+ *   kv_fused[g, d, r*F + j] = kv_head_mix[g, r] * k_proj[r, d, j]   ([G, D, R*F])
+ * Masters are float32; outputs are `dtype`.
+ * Replaces LeanSelectSelector.fused_weights (leanselect/selector.py:144-158).
+ */
+int ls_fused_weights(const float* head_mix, const float* kv_head_mix, const float* q_proj,
+                     const float* k_proj, int32_t num_heads, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t router_heads, int32_t router_dim, int32_t dtype,
+                     void* q_fused, void* kv_fused, void* stream);
+
+/*
+ * Workspace bytes needed by ls_project_queries / ls_project_atom_keys /
+ * ls_score_pages / ls_select_prefill.  Pass the sizes the call will see and 0
+ * for those it does not take (total_atoms and max_pages for
+ * ls_project_queries; total_q, batch and max_pages for ls_project_atom_keys;
+ * batch and max_pages for ls_score_pages).  max_pages = ceil(max_seqlen_q /
+ * block_size).
+ */
+size_t ls_select_workspace_size(int64_t total_q, int64_t total_atoms, int32_t batch,
+                                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                int32_t router_heads, int32_t router_dim, int32_t max_pages,
+                                int32_t dtype);
+
+/*
+ * GQA-group-summed query projection: out[g, n, f] =
+ *   sum_{s < H/G, d} query[n, g*H/G + s, d] * q_fused[g*H/G + s, d, f], rounded to dtype.
+ *   query [total_q, H, D] with rows `q_row_stride` elements apart; out [G, total_q, R*F].
+ * The fused weights are formed from the float32 masters inside the call.
+ * Replaces LeanSelectSelector.project_queries (leanselect/selector.py:160-177).
+ */
+int ls_project_queries(const void* query, int64_t q_row_stride, int64_t total_q,
+                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                       const float* head_mix, const float* q_proj, int32_t router_heads,
+                       int32_t router_dim, int32_t dtype, void* out, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/*
+ * Atom-key projection: out[g, a, f] = sum_d kc[a, g, d] * kv_fused[g, d, f].
+ *   kc [n_atoms, G, D] with rows `kc_row_stride` elements apart; out [G, n_atoms, R*F].
+ * Replaces LeanSelectSelector.project_atom_keys (leanselect/selector.py:179-190).
+ */
+int ls_project_atom_keys(const void* kc, int64_t kc_row_stride, int64_t n_atoms,
+                         int32_t num_kv_heads, int32_t head_dim, const float* kv_head_mix,
+                         const float* k_proj, int32_t router_heads, int32_t router_dim,
+                         int32_t dtype, void* out, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/*
+ * Page scores of one sequence: atom scores q~ . k~ (rounded to dtype) max-pooled
+ * over the overlapping window [p*s - 1, p*s + s) of atoms, s = block_size /
+ * kernel_stride, -inf where the window holds no atom.
+ *   query [n, H, D], kc [n_atoms, G, D], out [G, n, ceil(seq_len / block_size)].
+ * Replaces LeanSelectSelector.score_pages + pool_atoms_to_pages(reduce="max")
+ * (leanselect/selector.py:192-214; leanselect/pages.py:146-187).
+ */
+int ls_score_pages(const void* query, int64_t q_row_stride, int64_t n_queries,
+                   const void* kc, int64_t kc_row_stride, int64_t n_atoms, int32_t num_heads,
+                   int32_t num_kv_heads, int32_t head_dim, const float* head_mix,
+                   const float* kv_head_mix, const float* q_proj, const float* k_proj,
+                   int32_t router_heads, int32_t router_dim, int32_t dtype, int64_t seq_len,
+                   int32_t block_size, int32_t kernel_stride, void* out, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/*
+ * Page max-pool of atom scores: out[r, p] = max over atoms
+ * [p*pool_stride - 1, p*pool_stride + pool_stride) clipped to [0, n_atoms) of
+ * atom_scores[r, a] (-inf when empty); rows `row_stride` elements apart,
+ * out [rows, n_pages] contiguous.
+ * Replaces pool_atoms_to_pages(reduce="max") (leanselect/pages.py:146-187).
+ */
+int ls_pool_atoms_to_pages(const void* atom_scores, int64_t rows, int64_t n_atoms,
+                           int64_t row_stride, int32_t dtype, int64_t n_pages,
+                           int32_t pool_stride, void* out, void* stream);
+
+/*
+ * Forced-page mask: out[i, p] = p < init_blocks || (qp_i >= p && qp_i <= p + local_blocks)
+ * with qp_i = floor(positions[i] / block_size); positions int64 [n], out uint8 [n, num_pages].
+ * Replaces forced_page_mask (leanselect/pages.py:222-240).
+ */
+int ls_forced_page_mask(const int64_t* positions, int64_t n, int64_t num_pages,
+                        int32_t block_size, int32_t init_blocks, int32_t local_blocks,
+                        uint8_t* out, void* stream);
+
+/*
+ * Prefill page plans.  For each sequence b, query row t (relative page
+ * qp = t / block_size) and KV group g: pages p > qp are invisible, pages
+ * p < init_blocks and qp - local_blocks <= p <= qp are forced, and the
+ * remaining slots of take_b = min(take, ceil(len_q_b / block_size)) go to the
+ * highest page scores (ties to the lower page index).  Each row of
+ * topk_idx [G, total_q, take] (int32) lists its ids in ascending order and is
+ * padded with -1.  Rows of a sequence without query or compressed key are all -1.
+ *   q [total_q, H, D] (rows q_row_stride apart), kc [total_atoms, G, D] (rows
+ *   kc_row_stride apart), cu_seqlens_q / cu_seqlens_kc int32 [batch + 1],
+ *   take = min(topk, ceil(max_seqlen_q / block_size)).
+ * Replaces MiniCPMInfLLMv2Attention._lightweight_compressed_attention
+ * (leanselect/models/minicpm.py:3061-3142).
+ */
+int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t total_q, const void* kc,
+                      int64_t kc_row_stride, int64_t total_atoms, const int32_t* cu_seqlens_q,
+                      const int32_t* cu_seqlens_kc, int32_t batch, int32_t max_seqlen_q,
+                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                      const float* head_mix, const float* kv_head_mix, const float* q_proj,
+                      const float* k_proj, int32_t router_heads, int32_t router_dim,
+                      int32_t dtype, int32_t topk, int32_t block_size, int32_t kernel_stride,
+                      int32_t init_blocks, int32_t local_blocks, int32_t* topk_idx,
+                      int32_t take, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes needed by ls_sparse_attn_varlen.
+ */
+size_t ls_sparse_attn_workspace_size(int64_t total_k, int32_t batch, int32_t num_kv_heads,
+                                     int32_t head_dim, int32_t max_seqlen_k, int32_t dtype);
+
+/*
+ * Block-sparse attention over per-token page plans:
+ *   out[t, h] = softmax_j(scale * q[t, h] . k[j, h / (H/G)]) v[j, h / (H/G)]
+ * over keys j of the valid ids in topk_idx[h / (H/G), t, :] (each id once;
+ * -1 and out-of-range ids ignored) with, when causal, j <= t + len_k - len_q
+ * (relative to the sequence starts).  A row without any key gets out = 0 and
+ * lse = +inf.  lse [H, total_q] float32 (natural log) is written when non-null.
+ *   q [total_q, H, D], k / v [total_k, G, D] (rows *_row_stride apart),
+ *   topk_idx int32 [G, total_q, take], out [total_q, H, D] contiguous.
+ * Supports dtype LS_BF16 and LS_F16, head_dim 128, page (block) size 64.
+ * softmax_scale <= 0 selects head_dim^-0.5.
+ * Replaces infllmv2_attn_varlen_func(..., topk_idx=) (paper1.patch:1993-2100,
+ * called at leanselect/models/minicpm.py:3216-3244 and nosa.py:2213-2254).
+ */
+int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const void* k,
+                          int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                          const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                          int32_t batch, int64_t total_q, int64_t total_k, int32_t max_seqlen_q,
+                          int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t dtype, const int32_t* topk_idx,
+                          int32_t take, int32_t block_size, float softmax_scale,
+                          int32_t causal, void* out, float* lse, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LEANSELECT_HIP_H */

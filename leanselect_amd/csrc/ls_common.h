@@ -1,0 +1,119 @@
+// Shared device/host helpers for the gfx950 LeanSelect kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/leanselect_hip.h"
+
+#define LS_WAVE 64
+
+typedef __bf16 ls_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 ls_f16x8 __attribute__((ext_vector_type(8)));
+typedef float ls_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t ls_u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Host-side error plumbing (definitions in ls_runtime.hip).
+// ---------------------------------------------------------------------------
+int ls_fail(int code, const char* fmt, ...);
+int ls_check_launch(const char* what);
+
+#define LS_REQUIRE(cond, code, ...)          \
+  do {                                       \
+    if (!(cond)) return ls_fail((code), __VA_ARGS__); \
+  } while (0)
+
+static inline size_t ls_align256(size_t x) { return (x + 255) & ~(size_t)255; }
+static inline size_t ls_dtype_bytes(int dt) { return dt == LS_F32 ? 4 : 2; }
+static inline bool ls_aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// ---------------------------------------------------------------------------
+// Scalar conversions.  bf16 rounding is round-to-nearest-even of the float32
+// bit pattern (NaN -> canonical quiet NaN), which is what torch's float->bf16
+// cast does, so a kernel output rounds exactly like the reference's tensors.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float ls_bf16_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+
+__device__ __forceinline__ uint16_t ls_f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float ls_f16_to_f32(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+__device__ __forceinline__ uint16_t ls_f32_to_f16(float f) {
+  // Materialise the float32 value first: otherwise the compiler may fuse the
+  // producing multiply into a mixed-precision op that rounds once to fp16,
+  // which differs from torch's float32-then-fp16 double rounding on ties.
+  asm volatile("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Element traits: storage type, float conversions and the 16x16x32 MFMA.
+template <int DT> struct LsElem;
+
+template <> struct LsElem<LS_BF16> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float to_f(T v) { return ls_bf16_to_f32(v); }
+  static __device__ __forceinline__ T from_f(float v) { return ls_f32_to_bf16(v); }
+  static __device__ __forceinline__ ls_f32x4 mfma(ls_u32x4 a, ls_u32x4 b, ls_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(ls_bf16x8, a),
+                                                   __builtin_bit_cast(ls_bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <> struct LsElem<LS_F16> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float to_f(T v) { return ls_f16_to_f32(v); }
+  static __device__ __forceinline__ T from_f(float v) { return ls_f32_to_f16(v); }
+  static __device__ __forceinline__ ls_f32x4 mfma(ls_u32x4 a, ls_u32x4 b, ls_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(ls_f16x8, a),
+                                                  __builtin_bit_cast(ls_f16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <> struct LsElem<LS_F32> {
+  typedef float T;
+  static __device__ __forceinline__ float to_f(T v) { return v; }
+  static __device__ __forceinline__ T from_f(float v) { return v; }
+};
+
+// Two 16-bit values packed into one 32-bit lane register.
+__device__ __forceinline__ uint32_t ls_pack2(uint16_t lo, uint16_t hi) {
+  return (uint32_t)lo | ((uint32_t)hi << 16);
+}
+
+// 16-byte global load (8 half-width elements or 4 floats).
+__device__ __forceinline__ ls_u32x4 ls_load16(const void* p) {
+  return *reinterpret_cast<const ls_u32x4*>(p);
+}
+
+// Lane helpers.
+__device__ __forceinline__ int ls_lane() { return (int)__lane_id(); }
+
+__device__ __forceinline__ float ls_shfl(float v, int src_lane) {
+  return __shfl(v, src_lane, LS_WAVE);
+}
+
+__device__ __forceinline__ float ls_shfl_xor(float v, int mask) {
+  return __shfl_xor(v, mask, LS_WAVE);
+}
+
+// Index of the segment containing `x` in a nondecreasing prefix array
+// `off[0..n]` (off[0] == 0): largest b < n with off[b] <= x.
+__device__ __forceinline__ int ls_find_segment(const int32_t* off, int n, int64_t x) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)off[mid] <= x) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}

@@ -1,0 +1,735 @@
+// LeanSelect prefill selection on gfx950 (a2-a9).
+//
+//   fused weights  q_fused / kv_fused          leanselect/selector.py:144-158
+//   q~ = Q . q_fused summed over the GQA group leanselect/selector.py:160-177   (MFMA GEMM)
+//   k~ = Kc . kv_fused                         leanselect/selector.py:179-190   (MFMA GEMM)
+//   page score = max over a 5-atom window of   leanselect/selector.py:203-214,
+//                round(q~ . k~)                leanselect/pages.py:146-187       (MFMA + in-register pool)
+//   visibility, forced pages, top-k            leanselect/models/minicpm.py:3094-3142
+//
+// Rounding follows the reference: fused weights, q~, k~ and atom scores are
+// rounded to the activation dtype; a page score is the max of rounded atom
+// scores (rounding is monotone, so the max is rounded once).
+#include "ls_common.h"
+
+// ---------------------------------------------------------------------------
+// Fused weights
+// ---------------------------------------------------------------------------
+
+// Reference layout: q_fused[h][d][r*RD + j] = head_mix[h][r] * q_proj[r][d][j].
+template <int DT>
+__global__ __launch_bounds__(256) void ls_fuse_ref_kernel(
+    const float* __restrict__ mix, const float* __restrict__ proj, int heads, int R, int D,
+    int RD, typename LsElem<DT>::T* __restrict__ out) {
+  const int64_t F = (int64_t)R * RD;
+  const int64_t n = (int64_t)heads * D * F;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int f = (int)(i % F);
+  const int d = (int)((i / F) % D);
+  const int h = (int)(i / (F * D));
+  const int r = f / RD, j = f % RD;
+  out[i] = LsElem<DT>::from_f(mix[h * R + r] * proj[((int64_t)r * D + d) * RD + j]);
+}
+
+// GEMM layout: wt[g][f][s*D + d] = mix[g*gs + s][r] * proj[r][d][j] with f = r*RD + j,
+// i.e. the fused weights of one group transposed so the reduction index is
+// contiguous.  `heads = G * gs`.
+template <int DT>
+__global__ __launch_bounds__(256) void ls_fuse_t_kernel(
+    const float* __restrict__ mix, const float* __restrict__ proj, int G, int gs, int R, int D,
+    int RD, typename LsElem<DT>::T* __restrict__ wt) {
+  const int64_t F = (int64_t)R * RD;
+  const int64_t K = (int64_t)gs * D;
+  const int64_t n = (int64_t)G * F * K;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int k = (int)(i % K);
+  const int f = (int)((i / K) % F);
+  const int g = (int)(i / (K * F));
+  const int s = k / D, d = k % D;
+  const int r = f / RD, j = f % RD;
+  wt[i] = LsElem<DT>::from_f(mix[(g * gs + s) * R + r] * proj[((int64_t)r * D + d) * RD + j]);
+}
+
+// ---------------------------------------------------------------------------
+// Projection GEMM: out[g][m][f] = sum_k A[m*lda + g*gk + k] * wt[g][f][k].
+// 16-bit inputs on v_mfma_f32_16x16x32; each wave owns 32 rows x F columns.
+// Operand layout of the 16x16x32 MFMA (lane l, q = l / 16):
+//   A: row l%16, reduction slots 8q..8q+7;  B: column l%16, the same slots;
+//   D: rows 4q..4q+3, column l%16.
+// ---------------------------------------------------------------------------
+template <int DT, int FB>
+__global__ __launch_bounds__(256) void ls_proj_mfma_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, int64_t gk, int64_t M, int K,
+    const uint16_t* __restrict__ wt, uint16_t* __restrict__ out) {
+  constexpr int F = FB * 16;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int g = blockIdx.y;
+  const int64_t m0 = (int64_t)blockIdx.x * 128 + w * 32;
+  if (m0 >= M) return;
+  const uint16_t* Ag = A + g * gk;
+  const uint16_t* Wg = wt + (int64_t)g * F * K;
+  const int64_t row0 = min(m0 + r, M - 1), row1 = min(m0 + 16 + r, M - 1);
+  const uint16_t* a0p = Ag + row0 * lda + 8 * q;
+  const uint16_t* a1p = Ag + row1 * lda + 8 * q;
+  const uint16_t* bp = Wg + (int64_t)r * K + 8 * q;
+
+  ls_f32x4 acc0[FB], acc1[FB];
+#pragma unroll
+  for (int c = 0; c < FB; ++c) {
+    acc0[c] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
+    acc1[c] = acc0[c];
+  }
+  for (int k0 = 0; k0 < K; k0 += 32) {
+    const ls_u32x4 a0 = ls_load16(a0p + k0);
+    const ls_u32x4 a1 = ls_load16(a1p + k0);
+#pragma unroll
+    for (int c = 0; c < FB; ++c) {
+      const ls_u32x4 b = ls_load16(bp + (int64_t)c * 16 * K + k0);
+      acc0[c] = LsElem<DT>::mfma(a0, b, acc0[c]);
+      acc1[c] = LsElem<DT>::mfma(a1, b, acc1[c]);
+    }
+  }
+  uint16_t* og = out + (int64_t)g * M * F;
+#pragma unroll
+  for (int c = 0; c < FB; ++c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t ma = m0 + 4 * q + i, mb = m0 + 16 + 4 * q + i;
+      if (ma < M) og[ma * F + c * 16 + r] = LsElem<DT>::from_f(acc0[c][i]);
+      if (mb < M) og[mb * F + c * 16 + r] = LsElem<DT>::from_f(acc1[c][i]);
+    }
+  }
+}
+
+// float32 projection on the vector ALU (the reference's float32 path).
+__global__ __launch_bounds__(256) void ls_proj_f32_kernel(
+    const float* __restrict__ A, int64_t lda, int64_t gk, int64_t M, int K, int F,
+    const float* __restrict__ wt, float* __restrict__ out) {
+  const int g = blockIdx.y;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * F) return;
+  const int64_t m = i / F;
+  const int f = (int)(i % F);
+  const float* a = A + m * lda + g * gk;
+  const float* b = wt + ((int64_t)g * F + f) * K;
+  float acc = 0.f;
+  for (int k = 0; k < K; ++k) acc = fmaf(a[k], b[k], acc);
+  out[(int64_t)g * M * F + i] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Selection plan: blk_off[b] = sum_{b' < b} ceil(len_q(b') / block_size).
+// ---------------------------------------------------------------------------
+__global__ void ls_select_plan_kernel(const int32_t* __restrict__ cu_q, int batch, int bs,
+                                      int32_t* __restrict__ blk_off) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int32_t acc = 0;
+  blk_off[0] = 0;
+  for (int b = 0; b < batch; ++b) {
+    const int len = cu_q[b + 1] - cu_q[b];
+    acc += len > 0 ? (len + bs - 1) / bs : 0;
+    blk_off[b + 1] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Page scores on MFMA.  One workgroup = one 64-token query block of one KV
+// group; wave w owns tokens 16w..16w+15.  Atoms are the MFMA rows, tokens the
+// columns, so after one 16-atom step lane l (q = l/16) holds the four atoms
+// 16j+4q..16j+4q+3 of page 4j+q for token l%16; the fifth atom of the window
+// (16j+4q-1) is the last atom of the lane group below, one rotate away, or
+// the carry from the previous step for q == 0.
+//
+// SELECT: per sequence, only the non-forced visible pages
+// [init_blocks, qp - local_blocks - 1] of the block are scored, into the
+// scratch rows P[g][t][*].  FULL: a single sequence, every page, out[g][n][*].
+// ---------------------------------------------------------------------------
+template <int DT, int KS, bool SELECT>
+__global__ __launch_bounds__(256) void ls_score_mfma_kernel(
+    const uint16_t* __restrict__ qt, int64_t Nq, const uint16_t* __restrict__ kt, int64_t Na,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_a,
+    const int32_t* __restrict__ blk_off, int batch, int64_t n_blk_launch, int init_blocks,
+    int local_blocks, int64_t full_seq_len, uint16_t* __restrict__ out, int64_t out_stride) {
+  constexpr int F = KS * 32;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int g = blockIdx.y;
+
+  int64_t tq0, tq_end, a0, n_atoms;
+  int p_lo, p_hi;
+  if constexpr (SELECT) {
+    const int64_t ir = n_blk_launch - 1 - (int64_t)blockIdx.x;  // longest rows first
+    if (ir >= blk_off[batch]) return;
+    const int b = ls_find_segment(blk_off, batch, ir);
+    const int qb = (int)(ir - blk_off[b]);
+    tq0 = (int64_t)cu_q[b] + 64LL * qb;
+    tq_end = min(tq0 + 64, (int64_t)cu_q[b + 1]);
+    a0 = cu_a[b];
+    n_atoms = (int64_t)cu_a[b + 1] - a0;
+    p_lo = init_blocks;
+    p_hi = qb - local_blocks - 1;
+  } else {
+    tq0 = 64LL * blockIdx.x;
+    tq_end = min(tq0 + 64, Nq);
+    a0 = 0;
+    n_atoms = Na;
+    p_lo = 0;
+    p_hi = (int)((full_seq_len + 63) / 64) - 1;
+  }
+  if (n_atoms <= 0 || p_lo > p_hi) return;
+  const int64_t wt0 = tq0 + 16 * w;
+  if (wt0 >= tq_end) return;
+  const int64_t tok = min(wt0 + r, tq_end - 1);
+  const bool tok_ok = wt0 + r < tq_end;
+
+  ls_u32x4 qf[KS];
+  const uint16_t* qrow = qt + ((int64_t)g * Nq + tok) * F + 8 * q;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qf[ks] = ls_load16(qrow + 32 * ks);
+
+  const uint16_t* kbase = kt + ((int64_t)g * Na + a0) * F + 8 * q;
+  uint16_t* orow = out + ((int64_t)g * Nq + tok) * out_stride;
+  const int j_lo = p_lo >> 2, j_hi = p_hi >> 2;
+  float carry = -INFINITY;
+  for (int j = (j_lo > 0 ? j_lo - 1 : 0); j <= j_hi; ++j) {
+    const int64_t arow = min((int64_t)16 * j + r, n_atoms - 1);
+    const uint16_t* kp = kbase + arow * F;
+    ls_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) acc = LsElem<DT>::mfma(ls_load16(kp + 32 * ks), qf[ks], acc);
+    const int64_t atom0 = (int64_t)16 * j + 4 * q;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (atom0 + i >= n_atoms) acc[i] = -INFINITY;
+    const float m4 = fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3]));
+    const float rot = ls_shfl(acc[3], (lane - 16) & 63);
+    const float prev = q == 0 ? carry : rot;
+    carry = rot;
+    const int p = 4 * j + q;
+    if (j >= j_lo && p >= p_lo && p <= p_hi && tok_ok)
+      orow[p] = LsElem<DT>::from_f(fmaxf(m4, prev));
+  }
+}
+
+// float32 page scores on the vector ALU: one thread per (group, token, page).
+// General pooling stride s = block_size / kernel_stride.
+template <bool SELECT>
+__global__ __launch_bounds__(256) void ls_score_f32_kernel(
+    const float* __restrict__ qt, int64_t Nq, const float* __restrict__ kt, int64_t Na, int F,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_a, int batch,
+    int init_blocks, int local_blocks, int block_size, int s, int64_t full_seq_len,
+    int64_t n_pages_cols, float* __restrict__ out, int64_t out_stride) {
+  const int g = blockIdx.y;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= Nq * n_pages_cols) return;
+  const int64_t t = i / n_pages_cols;
+  const int p = (int)(i % n_pages_cols);
+  int64_t a0, n_atoms;
+  if constexpr (SELECT) {
+    const int b = ls_find_segment(cu_q, batch, t);
+    const int qp = (int)((t - cu_q[b]) / block_size);
+    if (p < init_blocks || p > qp - local_blocks - 1) return;
+    a0 = cu_a[b];
+    n_atoms = (int64_t)cu_a[b + 1] - a0;
+  } else {
+    if (p >= (full_seq_len + block_size - 1) / block_size) return;
+    a0 = 0;
+    n_atoms = Na;
+  }
+  if (n_atoms <= 0) return;
+  const float* qrow = qt + ((int64_t)g * Nq + t) * F;
+  float best = -INFINITY;
+  for (int64_t a = (int64_t)p * s - 1; a < (int64_t)p * s + s; ++a) {
+    if (a < 0 || a >= n_atoms) continue;
+    const float* krow = kt + ((int64_t)g * Na + a0 + a) * F;
+    float acc = 0.f;
+    for (int f = 0; f < F; ++f) acc = fmaf(qrow[f], krow[f], acc);
+    best = fmaxf(best, acc);
+  }
+  out[((int64_t)g * Nq + t) * out_stride + p] = best;
+}
+
+// ---------------------------------------------------------------------------
+// Top-k page selection.  One wave per (group, token) row.  The k'-th largest
+// order-preserving key T is found by bisection over the key bits, counting
+// with wave reductions over keys held in registers; pages above T and the
+// first (lowest-index) pages equal to T are emitted in ascending order
+// between the sink pages and the local pages.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t ls_order_key16(uint16_t b) {
+  return (b & 0x8000u) ? (~(uint32_t)b & 0xffffu) : ((uint32_t)b | 0x8000u);
+}
+__device__ __forceinline__ uint32_t ls_order_key32(uint32_t u) {
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ int ls_wave_sum(int v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, LS_WAVE);
+  return v;
+}
+
+template <int KPL, bool KEY32>
+__global__ __launch_bounds__(256) void ls_topk_kernel(
+    const void* __restrict__ P, int64_t p_stride, const int32_t* __restrict__ cu_q,
+    const int32_t* __restrict__ cu_a, int batch, int64_t total_q, int G, int take,
+    int init_blocks, int local_blocks, int block_size, int32_t* __restrict__ topk_idx) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (int64_t)G * total_q) return;
+  const int g = (int)(row / total_q);
+  const int64_t t = row - (int64_t)g * total_q;
+  int32_t* orow = topk_idx + row * take;
+  const int b = ls_find_segment(cu_q, batch, t);
+  const int64_t tr = t - cu_q[b];
+  const int lq = cu_q[b + 1] - cu_q[b];
+  const int n_atoms = cu_a[b + 1] - cu_a[b];
+  if (n_atoms <= 0) {
+    for (int i = lane; i < take; i += 64) orow[i] = -1;
+    return;
+  }
+  const int qp = (int)(tr / block_size);
+  const int n_pages = (lq + block_size - 1) / block_size;
+  const int take_b = min(take, n_pages);
+  const int n_valid = min(take_b, qp + 1);
+  const int lo_end = min(init_blocks, qp + 1);
+  const int hi_start = max(qp - local_blocks, lo_end);
+  const int n_forced = lo_end + (qp + 1 - hi_start);
+  for (int i = n_valid + lane; i < take; i += 64) orow[i] = -1;
+  if (n_forced >= n_valid) {
+    for (int i = lane; i < n_valid; i += 64) orow[i] = i < lo_end ? i : hi_start + (i - lo_end);
+    return;
+  }
+  const int kk = n_valid - n_forced;
+  const int cn = hi_start - lo_end;
+
+  uint32_t key[KPL];
+  const int64_t base = row * p_stride + lo_end;
+#pragma unroll
+  for (int s = 0; s < KPL; ++s) {
+    const int c = s * 64 + lane;
+    uint32_t k = 0;
+    if (c < cn) {
+      if constexpr (KEY32) k = ls_order_key32(((const uint32_t*)P)[base + c]);
+      else k = ls_order_key16(((const uint16_t*)P)[base + c]);
+    }
+    key[s] = k;
+  }
+  uint32_t T = 0;
+  for (int bit = KEY32 ? 31 : 15; bit >= 0; --bit) {
+    const uint32_t cand = T | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int s = 0; s < KPL; ++s) cnt += key[s] >= cand;
+    if (ls_wave_sum(cnt) >= kk) T = cand;
+  }
+  int gt = 0;
+#pragma unroll
+  for (int s = 0; s < KPL; ++s) gt += key[s] > T;
+  const int m = kk - ls_wave_sum(gt);
+
+  for (int i = lane; i < lo_end; i += 64) orow[i] = i;
+  const int hi_pos = lo_end + kk;
+  for (int i = lane; i < qp + 1 - hi_start; i += 64) orow[hi_pos + i] = hi_start + i;
+
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int out_pos = lo_end, eq_before = 0;
+#pragma unroll
+  for (int s = 0; s < KPL; ++s) {
+    const int c = s * 64 + lane;
+    const bool valid = c < cn;
+    const bool eq = valid && key[s] == T;
+    const uint64_t eq_mask = __ballot(eq);
+    const int eq_rank = eq_before + __popcll(eq_mask & lt_mask);
+    const bool sel = valid && (key[s] > T || (eq && eq_rank < m));
+    const uint64_t sel_mask = __ballot(sel);
+    if (sel) orow[out_pos + __popcll(sel_mask & lt_mask)] = lo_end + c;
+    out_pos += __popcll(sel_mask);
+    eq_before += __popcll(eq_mask);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+namespace {
+
+struct WsLayout {
+  size_t wq, wk, qt, kt, blk, p, total;
+  int64_t p_stride;
+};
+
+WsLayout ws_layout(int64_t total_q, int64_t total_atoms, int batch, int H, int G, int D, int F,
+                   int max_pages, int eb) {
+  WsLayout L;
+  size_t off = 0;
+  L.wq = off; off += ls_align256((size_t)H * D * F * eb);
+  L.wk = off; off += ls_align256((size_t)G * D * F * eb);
+  L.qt = off; off += ls_align256((size_t)G * total_q * F * eb);
+  L.kt = off; off += ls_align256((size_t)G * total_atoms * F * eb);
+  L.blk = off; off += ls_align256((size_t)(batch + 1) * 4);
+  L.p_stride = ((int64_t)max_pages + 63) & ~(int64_t)63;
+  L.p = off; off += ls_align256((size_t)G * total_q * L.p_stride * eb);
+  L.total = off;
+  return L;
+}
+
+int check_dims(const char* who, int H, int G, int D, int R, int RD, int dtype) {
+  LS_REQUIRE(H > 0 && G > 0 && D > 0 && R > 0 && RD > 0, LS_ERR_INVALID, "%s: bad sizes", who);
+  LS_REQUIRE(H % G == 0, LS_ERR_INVALID, "%s: num_heads must be divisible by num_kv_heads", who);
+  LS_REQUIRE(R <= H, LS_ERR_INVALID, "%s: router_heads cannot exceed num_heads", who);
+  LS_REQUIRE(dtype == LS_F32 || dtype == LS_BF16 || dtype == LS_F16, LS_ERR_INVALID,
+             "%s: unknown dtype %d", who, dtype);
+  if (dtype != LS_F32) {
+    const int F = R * RD;
+    LS_REQUIRE(D % 32 == 0 && F % 32 == 0 && F <= 256, LS_ERR_UNSUPPORTED,
+               "%s: 16-bit path needs head_dim %% 32 == 0 and router width in {32..256} "
+               "step 32 (got D=%d F=%d)", who, D, F);
+  }
+  return LS_OK;
+}
+
+template <int DT>
+int launch_fuse_t(const float* mix, const float* proj, int G, int gs, int R, int D, int RD,
+                  void* wt, hipStream_t s) {
+  const int64_t n = (int64_t)G * gs * D * R * RD;
+  hipLaunchKernelGGL(ls_fuse_t_kernel<DT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     mix, proj, G, gs, R, D, RD, (typename LsElem<DT>::T*)wt);
+  return ls_check_launch("ls_fuse_t_kernel");
+}
+
+int fuse_t(int dtype, const float* mix, const float* proj, int G, int gs, int R, int D, int RD,
+           void* wt, hipStream_t s) {
+  switch (dtype) {
+    case LS_BF16: return launch_fuse_t<LS_BF16>(mix, proj, G, gs, R, D, RD, wt, s);
+    case LS_F16: return launch_fuse_t<LS_F16>(mix, proj, G, gs, R, D, RD, wt, s);
+    default: return launch_fuse_t<LS_F32>(mix, proj, G, gs, R, D, RD, wt, s);
+  }
+}
+
+template <int DT>
+int launch_proj16(const void* A, int64_t lda, int64_t gk, int64_t M, int K, int F, int G,
+                  const void* wt, void* out, hipStream_t s) {
+  const dim3 grid((unsigned)((M + 127) / 128), G);
+  const uint16_t* a = (const uint16_t*)A;
+  const uint16_t* w = (const uint16_t*)wt;
+  uint16_t* o = (uint16_t*)out;
+  switch (F / 16) {
+    case 2: hipLaunchKernelGGL((ls_proj_mfma_kernel<DT, 2>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o); break;
+    case 4: hipLaunchKernelGGL((ls_proj_mfma_kernel<DT, 4>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o); break;
+    case 6: hipLaunchKernelGGL((ls_proj_mfma_kernel<DT, 6>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o); break;
+    case 8: hipLaunchKernelGGL((ls_proj_mfma_kernel<DT, 8>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o); break;
+    case 10: hipLaunchKernelGGL((ls_proj_mfma_kernel<DT, 10>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o); break;
+    case 12: hipLaunchKernelGGL((ls_proj_mfma_kernel<DT, 12>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o); break;
+    case 14: hipLaunchKernelGGL((ls_proj_mfma_kernel<DT, 14>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o); break;
+    case 16: hipLaunchKernelGGL((ls_proj_mfma_kernel<DT, 16>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o); break;
+    default: return ls_fail(LS_ERR_UNSUPPORTED, "projection: router width %d unsupported", F);
+  }
+  return ls_check_launch("ls_proj_mfma_kernel");
+}
+
+// out[g][m][:] = A-rows . wt[g]; K = reduction length; A rows lda apart, group g at g*gk.
+int project(int dtype, const void* A, int64_t lda, int64_t gk, int64_t M, int K, int F, int G,
+            const void* wt, void* out, hipStream_t s) {
+  if (M == 0) return LS_OK;
+  if (dtype == LS_F32) {
+    const dim3 grid((unsigned)((M * F + 255) / 256), G);
+    hipLaunchKernelGGL(ls_proj_f32_kernel, grid, dim3(256), 0, s, (const float*)A, lda, gk, M,
+                       K, F, (const float*)wt, (float*)out);
+    return ls_check_launch("ls_proj_f32_kernel");
+  }
+  LS_REQUIRE(ls_aligned16(A) && lda % 8 == 0 && gk % 8 == 0, LS_ERR_UNSUPPORTED,
+             "projection: 16-bit inputs must be 16-byte aligned with row strides %% 8 == 0");
+  if (dtype == LS_BF16) return launch_proj16<LS_BF16>(A, lda, gk, M, K, F, G, wt, out, s);
+  return launch_proj16<LS_F16>(A, lda, gk, M, K, F, G, wt, out, s);
+}
+
+template <int DT, bool SELECT>
+int launch_score16(int F, dim3 grid, hipStream_t s, const void* qt, int64_t Nq, const void* kt,
+                   int64_t Na, const int32_t* cu_q, const int32_t* cu_a, const int32_t* blk,
+                   int batch, int64_t n_launch, int init_blocks, int local_blocks,
+                   int64_t full_len, void* out, int64_t out_stride) {
+  const uint16_t* qp = (const uint16_t*)qt;
+  const uint16_t* kp = (const uint16_t*)kt;
+  uint16_t* op = (uint16_t*)out;
+  switch (F / 32) {
+#define LS_SCORE_CASE(KSV)                                                                   \
+  case KSV:                                                                                  \
+    hipLaunchKernelGGL((ls_score_mfma_kernel<DT, KSV, SELECT>), grid, dim3(256), 0, s, qp, Nq, \
+                       kp, Na, cu_q, cu_a, blk, batch, n_launch, init_blocks, local_blocks,    \
+                       full_len, op, out_stride);                                            \
+    break;
+    LS_SCORE_CASE(1)
+    LS_SCORE_CASE(2)
+    LS_SCORE_CASE(3)
+    LS_SCORE_CASE(4)
+    LS_SCORE_CASE(5)
+    LS_SCORE_CASE(6)
+    LS_SCORE_CASE(7)
+    LS_SCORE_CASE(8)
+#undef LS_SCORE_CASE
+    default: return ls_fail(LS_ERR_UNSUPPORTED, "score: router width %d unsupported", F);
+  }
+  return ls_check_launch("ls_score_mfma_kernel");
+}
+
+template <bool SELECT>
+int score(int dtype, int F, const void* qt, int64_t Nq, const void* kt, int64_t Na,
+          const int32_t* cu_q, const int32_t* cu_a, const int32_t* blk, int batch,
+          int64_t n_blk_launch, int init_blocks, int local_blocks, int block_size,
+          int kernel_stride, int64_t full_len, int64_t n_page_cols, void* out,
+          int64_t out_stride, int G, hipStream_t s) {
+  if (Nq == 0) return LS_OK;
+  if (dtype == LS_F32) {
+    const int64_t n = Nq * n_page_cols;
+    const dim3 grid((unsigned)((n + 255) / 256), G);
+    hipLaunchKernelGGL(ls_score_f32_kernel<SELECT>, grid, dim3(256), 0, s, (const float*)qt, Nq,
+                       (const float*)kt, Na, F, cu_q, cu_a, batch, init_blocks, local_blocks,
+                       block_size, block_size / kernel_stride, full_len, n_page_cols,
+                       (float*)out, out_stride);
+    return ls_check_launch("ls_score_f32_kernel");
+  }
+  LS_REQUIRE(block_size == 64 && kernel_stride == 16, LS_ERR_UNSUPPORTED,
+             "score: the 16-bit path supports block_size 64 with kernel_stride 16 "
+             "(got %d/%d)", block_size, kernel_stride);
+  const dim3 grid(SELECT ? (unsigned)n_blk_launch : (unsigned)((Nq + 63) / 64), G);
+  if (dtype == LS_BF16)
+    return launch_score16<LS_BF16, SELECT>(F, grid, s, qt, Nq, kt, Na, cu_q, cu_a, blk, batch,
+                                           n_blk_launch, init_blocks, local_blocks, full_len,
+                                           out, out_stride);
+  return launch_score16<LS_F16, SELECT>(F, grid, s, qt, Nq, kt, Na, cu_q, cu_a, blk, batch,
+                                        n_blk_launch, init_blocks, local_blocks, full_len, out,
+                                        out_stride);
+}
+
+template <int KPL, bool KEY32>
+void launch_topk_kpl(dim3 grid, hipStream_t s, const void* P, int64_t ps, const int32_t* cu_q,
+                     const int32_t* cu_a, int batch, int64_t total_q, int G, int take, int init,
+                     int local, int bs, int32_t* out) {
+  hipLaunchKernelGGL((ls_topk_kernel<KPL, KEY32>), grid, dim3(256), 0, s, P, ps, cu_q, cu_a,
+                     batch, total_q, G, take, init, local, bs, out);
+}
+
+template <bool KEY32>
+int launch_topk(int max_pages, dim3 grid, hipStream_t s, const void* P, int64_t ps,
+                const int32_t* cu_q, const int32_t* cu_a, int batch, int64_t total_q, int G,
+                int take, int init, int local, int bs, int32_t* out) {
+  if (max_pages <= 256)
+    launch_topk_kpl<4, KEY32>(grid, s, P, ps, cu_q, cu_a, batch, total_q, G, take, init, local, bs, out);
+  else if (max_pages <= 1024)
+    launch_topk_kpl<16, KEY32>(grid, s, P, ps, cu_q, cu_a, batch, total_q, G, take, init, local, bs, out);
+  else if (max_pages <= 2048)
+    launch_topk_kpl<32, KEY32>(grid, s, P, ps, cu_q, cu_a, batch, total_q, G, take, init, local, bs, out);
+  else if (max_pages <= 4096)
+    launch_topk_kpl<64, KEY32>(grid, s, P, ps, cu_q, cu_a, batch, total_q, G, take, init, local, bs, out);
+  else if (max_pages <= 8192)
+    launch_topk_kpl<128, KEY32>(grid, s, P, ps, cu_q, cu_a, batch, total_q, G, take, init, local, bs, out);
+  else
+    return ls_fail(LS_ERR_UNSUPPORTED, "select: at most 8192 pages per sequence (got %d)", max_pages);
+  return ls_check_launch("ls_topk_kernel");
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" size_t ls_select_workspace_size(int64_t total_q, int64_t total_atoms, int32_t batch,
+                                           int32_t num_heads, int32_t num_kv_heads,
+                                           int32_t head_dim, int32_t router_heads,
+                                           int32_t router_dim, int32_t max_pages,
+                                           int32_t dtype) {
+  return ws_layout(total_q, total_atoms, batch, num_heads, num_kv_heads, head_dim,
+                   router_heads * router_dim, max_pages, (int)ls_dtype_bytes(dtype))
+      .total;
+}
+
+extern "C" int ls_fused_weights(const float* head_mix, const float* kv_head_mix,
+                                const float* q_proj, const float* k_proj, int32_t num_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t router_heads,
+                                int32_t router_dim, int32_t dtype, void* q_fused,
+                                void* kv_fused, void* stream) {
+  LS_REQUIRE(num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && router_heads > 0 &&
+                 router_dim > 0,
+             LS_ERR_INVALID, "ls_fused_weights: bad sizes");
+  LS_REQUIRE(dtype == LS_F32 || dtype == LS_BF16 || dtype == LS_F16, LS_ERR_INVALID,
+             "ls_fused_weights: unknown dtype %d", dtype);
+  LS_REQUIRE(head_mix && kv_head_mix && q_proj && k_proj && q_fused && kv_fused, LS_ERR_INVALID,
+             "ls_fused_weights: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t F = (int64_t)router_heads * router_dim;
+  const int64_t nq = (int64_t)num_heads * head_dim * F, nk = (int64_t)num_kv_heads * head_dim * F;
+#define LS_FUSE(DT, TT)                                                                         \
+  hipLaunchKernelGGL(ls_fuse_ref_kernel<DT>, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, \
+                     head_mix, q_proj, num_heads, router_heads, head_dim, router_dim, (TT*)q_fused); \
+  hipLaunchKernelGGL(ls_fuse_ref_kernel<DT>, dim3((unsigned)((nk + 255) / 256)), dim3(256), 0, s, \
+                     kv_head_mix, k_proj, num_kv_heads, router_heads, head_dim, router_dim,        \
+                     (TT*)kv_fused);
+  if (dtype == LS_BF16) { LS_FUSE(LS_BF16, uint16_t) }
+  else if (dtype == LS_F16) { LS_FUSE(LS_F16, uint16_t) }
+  else { LS_FUSE(LS_F32, float) }
+#undef LS_FUSE
+  return ls_check_launch("ls_fuse_ref_kernel");
+}
+
+extern "C" int ls_project_queries(const void* query, int64_t q_row_stride, int64_t total_q,
+                                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  const float* head_mix, const float* q_proj,
+                                  int32_t router_heads, int32_t router_dim, int32_t dtype,
+                                  void* out, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  int rc = check_dims("ls_project_queries", num_heads, num_kv_heads, head_dim, router_heads,
+                      router_dim, dtype);
+  if (rc) return rc;
+  LS_REQUIRE(total_q >= 0 && (total_q == 0 || (query && out)), LS_ERR_INVALID,
+             "ls_project_queries: null tensor");
+  const int eb = (int)ls_dtype_bytes(dtype);
+  const int F = router_heads * router_dim, G = num_kv_heads, gs = num_heads / num_kv_heads;
+  const WsLayout L = ws_layout(0, 0, 0, num_heads, G, head_dim, F, 0, eb);
+  LS_REQUIRE(workspace && workspace_bytes >= L.total, LS_ERR_WORKSPACE,
+             "ls_project_queries: workspace needs %zu bytes", L.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  rc = fuse_t(dtype, head_mix, q_proj, G, gs, router_heads, head_dim, router_dim, ws + L.wq, s);
+  if (rc) return rc;
+  return project(dtype, query, q_row_stride, (int64_t)gs * head_dim, total_q, gs * head_dim, F,
+                 G, ws + L.wq, out, s);
+}
+
+extern "C" int ls_project_atom_keys(const void* kc, int64_t kc_row_stride, int64_t n_atoms,
+                                    int32_t num_kv_heads, int32_t head_dim,
+                                    const float* kv_head_mix, const float* k_proj,
+                                    int32_t router_heads, int32_t router_dim, int32_t dtype,
+                                    void* out, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  int rc = check_dims("ls_project_atom_keys", num_kv_heads, num_kv_heads, head_dim,
+                      router_heads > num_kv_heads ? 1 : router_heads, router_dim, dtype);
+  if (rc) return rc;
+  LS_REQUIRE(router_heads > 0, LS_ERR_INVALID, "ls_project_atom_keys: bad router_heads");
+  LS_REQUIRE(n_atoms >= 0 && (n_atoms == 0 || (kc && out)), LS_ERR_INVALID,
+             "ls_project_atom_keys: null tensor");
+  const int eb = (int)ls_dtype_bytes(dtype);
+  const int F = router_heads * router_dim, G = num_kv_heads;
+  LS_REQUIRE(dtype == LS_F32 || (F % 32 == 0 && F <= 256), LS_ERR_UNSUPPORTED,
+             "ls_project_atom_keys: router width %d unsupported on the 16-bit path", F);
+  const WsLayout L = ws_layout(0, 0, 0, G, G, head_dim, F, 0, eb);
+  LS_REQUIRE(workspace && workspace_bytes >= L.total, LS_ERR_WORKSPACE,
+             "ls_project_atom_keys: workspace needs %zu bytes", L.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  rc = fuse_t(dtype, kv_head_mix, k_proj, G, 1, router_heads, head_dim, router_dim, ws + L.wk, s);
+  if (rc) return rc;
+  return project(dtype, kc, kc_row_stride, head_dim, n_atoms, head_dim, F, G, ws + L.wk, out, s);
+}
+
+extern "C" int ls_score_pages(const void* query, int64_t q_row_stride, int64_t n_queries,
+                              const void* kc, int64_t kc_row_stride, int64_t n_atoms,
+                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                              const float* head_mix, const float* kv_head_mix,
+                              const float* q_proj, const float* k_proj, int32_t router_heads,
+                              int32_t router_dim, int32_t dtype, int64_t seq_len,
+                              int32_t block_size, int32_t kernel_stride, void* out,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_dims("ls_score_pages", num_heads, num_kv_heads, head_dim, router_heads,
+                      router_dim, dtype);
+  if (rc) return rc;
+  LS_REQUIRE(seq_len > 0 && block_size > 0 && kernel_stride > 0, LS_ERR_INVALID,
+             "ls_score_pages: page geometry must be positive");
+  LS_REQUIRE(block_size % kernel_stride == 0, LS_ERR_INVALID,
+             "ls_score_pages: block_size must be divisible by kernel_stride");
+  LS_REQUIRE(n_atoms > 0, LS_ERR_INVALID, "ls_score_pages: need at least one atom");
+  const int eb = (int)ls_dtype_bytes(dtype);
+  const int F = router_heads * router_dim, G = num_kv_heads, gs = num_heads / num_kv_heads;
+  const WsLayout L = ws_layout(n_queries, n_atoms, 0, num_heads, G, head_dim, F, 0, eb);
+  LS_REQUIRE(workspace && workspace_bytes >= L.total, LS_ERR_WORKSPACE,
+             "ls_score_pages: workspace needs %zu bytes", L.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  if ((rc = fuse_t(dtype, head_mix, q_proj, G, gs, router_heads, head_dim, router_dim,
+                   ws + L.wq, s)))
+    return rc;
+  if ((rc = fuse_t(dtype, kv_head_mix, k_proj, G, 1, router_heads, head_dim, router_dim,
+                   ws + L.wk, s)))
+    return rc;
+  if ((rc = project(dtype, query, q_row_stride, (int64_t)gs * head_dim, n_queries,
+                    gs * head_dim, F, G, ws + L.wq, ws + L.qt, s)))
+    return rc;
+  if ((rc = project(dtype, kc, kc_row_stride, head_dim, n_atoms, head_dim, F, G, ws + L.wk,
+                    ws + L.kt, s)))
+    return rc;
+  const int64_t n_pages = (seq_len + block_size - 1) / block_size;
+  return score<false>(dtype, F, ws + L.qt, n_queries, ws + L.kt, n_atoms, nullptr, nullptr,
+                      nullptr, 0, 0, 0, 0, block_size, kernel_stride, seq_len, n_pages, out,
+                      n_pages, G, s);
+}
+
+extern "C" int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t total_q,
+                                 const void* kc, int64_t kc_row_stride, int64_t total_atoms,
+                                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kc,
+                                 int32_t batch, int32_t max_seqlen_q, int32_t num_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, const float* head_mix,
+                                 const float* kv_head_mix, const float* q_proj,
+                                 const float* k_proj, int32_t router_heads, int32_t router_dim,
+                                 int32_t dtype, int32_t topk, int32_t block_size,
+                                 int32_t kernel_stride, int32_t init_blocks,
+                                 int32_t local_blocks, int32_t* topk_idx, int32_t take,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_dims("ls_select_prefill", num_heads, num_kv_heads, head_dim, router_heads,
+                      router_dim, dtype);
+  if (rc) return rc;
+  LS_REQUIRE(batch >= 0 && total_q >= 0 && total_atoms >= 0 && max_seqlen_q >= 0, LS_ERR_INVALID,
+             "ls_select_prefill: bad sizes");
+  LS_REQUIRE(block_size > 0 && kernel_stride > 0 && block_size % kernel_stride == 0,
+             LS_ERR_INVALID, "ls_select_prefill: bad page geometry");
+  LS_REQUIRE(init_blocks >= 0 && local_blocks >= 0 && topk >= 0, LS_ERR_INVALID,
+             "ls_select_prefill: init_blocks, local_blocks and topk must be >= 0");
+  const int max_pages = (max_seqlen_q + block_size - 1) / block_size;
+  LS_REQUIRE(take == (topk < max_pages ? topk : max_pages), LS_ERR_INVALID,
+             "ls_select_prefill: take must be min(topk, ceil(max_seqlen_q / block_size)) = %d",
+             topk < max_pages ? topk : max_pages);
+  if (total_q == 0 || batch == 0 || take == 0) return LS_OK;
+  LS_REQUIRE(q && kc && cu_seqlens_q && cu_seqlens_kc && topk_idx, LS_ERR_INVALID,
+             "ls_select_prefill: null pointer");
+  const int eb = (int)ls_dtype_bytes(dtype);
+  const int F = router_heads * router_dim, G = num_kv_heads, gs = num_heads / num_kv_heads;
+  const WsLayout L = ws_layout(total_q, total_atoms, batch, num_heads, G, head_dim, F,
+                               max_pages, eb);
+  LS_REQUIRE(workspace && workspace_bytes >= L.total, LS_ERR_WORKSPACE,
+             "ls_select_prefill: workspace needs %zu bytes", L.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  int32_t* blk = (int32_t*)(ws + L.blk);
+  if ((rc = fuse_t(dtype, head_mix, q_proj, G, gs, router_heads, head_dim, router_dim,
+                   ws + L.wq, s)))
+    return rc;
+  if ((rc = fuse_t(dtype, kv_head_mix, k_proj, G, 1, router_heads, head_dim, router_dim,
+                   ws + L.wk, s)))
+    return rc;
+  if ((rc = project(dtype, q, q_row_stride, (int64_t)gs * head_dim, total_q, gs * head_dim, F,
+                    G, ws + L.wq, ws + L.qt, s)))
+    return rc;
+  if (total_atoms > 0 &&
+      (rc = project(dtype, kc, kc_row_stride, head_dim, total_atoms, head_dim, F, G, ws + L.wk,
+                    ws + L.kt, s)))
+    return rc;
+  hipLaunchKernelGGL(ls_select_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens_q, batch,
+                     block_size, blk);
+  if ((rc = ls_check_launch("ls_select_plan_kernel"))) return rc;
+  const int64_t n_blk_launch = (total_q + block_size - 1) / block_size + batch;
+  if (total_atoms > 0 &&
+      (rc = score<true>(dtype, F, ws + L.qt, total_q, ws + L.kt, total_atoms, cu_seqlens_q,
+                        cu_seqlens_kc, blk, batch, n_blk_launch, init_blocks, local_blocks,
+                        block_size, kernel_stride, 0, max_pages, ws + L.p, L.p_stride, G, s)))
+    return rc;
+  const dim3 grid((unsigned)(((int64_t)G * total_q + 3) / 4));
+  if (dtype == LS_F32)
+    return launch_topk<true>(max_pages, grid, s, ws + L.p, L.p_stride, cu_seqlens_q,
+                             cu_seqlens_kc, batch, total_q, G, take, init_blocks, local_blocks,
+                             block_size, topk_idx);
+  return launch_topk<false>(max_pages, grid, s, ws + L.p, L.p_stride, cu_seqlens_q,
+                            cu_seqlens_kc, batch, total_q, G, take, init_blocks, local_blocks,
+                            block_size, topk_idx);
+}

@@ -1,0 +1,15 @@
+"""GPU operators of the LeanSelect prefill hot path (mirror of ``leanselect.ops``)."""
+from .attention import infllmv2_attn_varlen_func, sparse_attention
+from .compress import CompressK, compress_k
+from .select import leanselect_prefill_topk_idx, select_take
+from . import profiling
+
+__all__ = [
+    "CompressK",
+    "compress_k",
+    "leanselect_prefill_topk_idx",
+    "select_take",
+    "infllmv2_attn_varlen_func",
+    "sparse_attention",
+    "profiling",
+]

@@ -1,0 +1,160 @@
+"""GPU parity of page selection and block-sparse attention against the oracle,
+on the benchmark's synthetic workloads (small sizes in full, 32K on sampled rows
+plus size-independent plan invariants)."""
+import pytest
+import torch
+
+import oracle
+from gpu_helpers import oracle_select_rows, plan_structure_errors, spread_rows
+from leanselect_amd import workloads
+from leanselect_amd.ops import compress_k, leanselect_prefill_topk_idx, sparse_attention
+from leanselect_amd.ops.attention import infllmv2_attn_varlen_func
+from leanselect_amd.prefill import leanselect_sparse_prefill
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _select(case):
+    kc, cu_c = compress_k(case.k, case.cu_seqlens, cu_seqlens_host=case.cu_host)
+    ids = leanselect_prefill_topk_idx(
+        case.q, kc, case.cu_seqlens, cu_c, case.selector, topk=case.topk,
+        init_blocks=case.init_blocks, local_blocks=case.local_blocks, cu_seqlens_q_host=case.cu_host)
+    return kc, cu_c, ids
+
+
+def _check_select(case, rows=None):
+    kc, cu_c, ids = _select(case)
+    take = ids.shape[-1]
+    errs = plan_structure_errors(ids, case.cu_host, take, case.init_blocks, case.local_blocks)
+    assert not errs, errs
+    kc_cpu = kc.cpu()
+    want_kc, want_cu = oracle.compress_k(case.k.cpu(), case.cu_host)
+    assert cu_c.cpu().tolist() == want_cu.tolist()
+    if case.q.dtype == torch.float32:
+        torch.testing.assert_close(kc_cpu, want_kc, rtol=2e-6, atol=1e-6)
+    # Parity of the plans uses the GPU's compressed keys so the rows test selection alone.
+    want_ids, scores = oracle_select_rows(case, kc_cpu, cu_c.cpu().tolist(), rows, case.q.dtype)
+    got = ids.cpu() if rows is None else ids.cpu()[:, rows]
+    rep = oracle.check_topk(got, want_ids, scores, case.q.dtype)
+    print(f"\nselect parity: {rep}")
+    assert rep.ok, str(rep)
+    return kc, cu_c, ids, rep
+
+
+def test_select_head_space_fp32_4k():
+    case = workloads.head_space_layer(4096, device=DEV)
+    _, _, ids, rep = _check_select(case)
+    assert ids.shape == (2, 4096, 16)
+    assert rep.exact_rows == rep.rows  # float32: every row bit-exact
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_select_hidden_space_4k(dtype):
+    case = workloads.hidden_space_layer((4096,), device=DEV, dtype=dtype, seed=1)
+    _, _, ids, rep = _check_select(case)
+    assert ids.shape == (2, 4096, 64)
+    assert rep.exact_rows >= 0.97 * rep.rows
+
+
+def test_select_ragged_with_short_sequences():
+    lens = (8, 31, 32, 100, 1000, 2113, 64, 0, 4500)
+    case = workloads.hidden_space_layer(lens, device=DEV, seed=2)
+    _, _, ids, rep = _check_select(case)
+    cu = case.cu_host
+    # Sequences shorter than one compression window get no plan at all.
+    for b, n in enumerate(lens):
+        if 0 < n < 32:
+            assert bool((ids[:, cu[b] : cu[b + 1]] == -1).all())
+
+
+def test_select_32k_sampled_rows():
+    case = workloads.hidden_space_layer((32768,), device=DEV, seed=3)
+    rows = spread_rows(case.cu_host, per_seq=128)
+    _, _, ids, rep = _check_select(case, rows=rows)
+    assert rep.exact_rows >= 0.97 * rep.rows
+
+
+def _attention_case(dtype=torch.bfloat16, lens=(3000,), seed=4, **kw):
+    case = workloads.hidden_space_layer(lens, device=DEV, dtype=dtype, seed=seed, **kw)
+    _, _, ids = _select(case)
+    return case, ids
+
+
+def _check_attention(case, ids, rows, **kw):
+    out, lse = sparse_attention(case.q, case.k, case.v, case.cu_seqlens, case.cu_seqlens,
+                                case.max_seqlen, case.max_seqlen, ids, return_lse=True, **kw)
+    want, want_lse = oracle.sparse_attention(
+        case.q.cpu(), case.k.cpu(), case.v.cpu(), case.cu_host, case.cu_host,
+        ids.cpu()[:, rows], rows=rows, ids_rows_aligned=True, **kw)
+    ok, mx, mr = oracle.check_attention(out.cpu()[rows], want)
+    print(f"\nattention parity: max_abs={mx:.3e} mean_rel={mr:.3e}")
+    assert ok, (mx, mr)
+    got_lse = lse.cpu()[:, rows]
+    fin = torch.isfinite(want_lse)
+    assert torch.equal(torch.isfinite(got_lse), fin)
+    torch.testing.assert_close(got_lse[fin], want_lse[fin], rtol=1e-4, atol=2e-3)
+    return out
+
+
+def test_attention_matches_oracle_bf16():
+    case, ids = _attention_case()
+    rows = spread_rows(case.cu_host, per_seq=64)
+    _check_attention(case, ids, rows)
+
+
+def test_attention_fp16_and_scale():
+    case, ids = _attention_case(dtype=torch.float16, seed=5)
+    rows = spread_rows(case.cu_host, per_seq=48)
+    _check_attention(case, ids, rows, softmax_scale=0.05)
+
+
+def test_attention_ragged_batch():
+    case, ids = _attention_case(lens=(1, 31, 65, 700, 2000), seed=6)
+    rows = spread_rows(case.cu_host, per_seq=40)
+    out = _check_attention(case, ids, rows)
+    # Rows without any page (sequences shorter than a compression window) are zero.
+    assert bool((out[:32] == 0).all())
+
+
+def test_attention_messy_ids_duplicates_unsorted_out_of_range():
+    case, ids = _attention_case(lens=(1500,), seed=7)
+    g = torch.Generator(device="cpu").manual_seed(0)
+    G, N, T = ids.shape
+    messy = torch.randint(-3, 30, (G, N, T), generator=g, dtype=torch.int32)
+    messy[..., 0] = messy[..., 1]  # duplicates
+    rows = spread_rows(case.cu_host, per_seq=40)
+    _check_attention(case, messy.to(DEV), rows)
+
+
+def test_attention_group_size_4_and_non_causal():
+    case = workloads.head_space_layer(1024, device=DEV, dtype=torch.bfloat16)
+    _, _, ids = _select(case)
+    rows = spread_rows(case.cu_host, per_seq=40)
+    _check_attention(case, ids, rows)
+    _check_attention(case, ids, rows, causal=False)
+
+
+def test_infllm_surface_returns_lse_tuple():
+    case, ids = _attention_case(lens=(700,), seed=8)
+    out = infllmv2_attn_varlen_func(case.q, case.k, case.v, case.cu_seqlens, case.cu_seqlens,
+                                    700, 700, causal=True, topk_idx=ids)
+    out2, lse, s = infllmv2_attn_varlen_func(case.q, case.k, case.v, case.cu_seqlens,
+                                             case.cu_seqlens, 700, 700, causal=True,
+                                             return_attn_probs=True, topk_idx=ids)
+    assert torch.equal(out, out2) and lse.shape == (32, 700) and s.numel() == 0
+
+
+def test_end_to_end_prefill_32k_sampled():
+    case = workloads.hidden_space_layer((32768,), device=DEV, seed=9)
+    out, ids = leanselect_sparse_prefill(
+        case.q, case.k, case.v, case.cu_seqlens, case.selector, topk=case.topk,
+        local_blocks=case.local_blocks, init_blocks=case.init_blocks,
+        cu_seqlens_host=case.cu_host, return_topk_idx=True)
+    assert not plan_structure_errors(ids, case.cu_host, 64, 1, 4)
+    rows = spread_rows(case.cu_host, per_seq=24)
+    want, _ = oracle.sparse_attention(case.q.cpu(), case.k.cpu(), case.v.cpu(), case.cu_host,
+                                      case.cu_host, ids.cpu()[:, rows], rows=rows,
+                                      ids_rows_aligned=True)
+    ok, mx, mr = oracle.check_attention(out.cpu()[rows], want)
+    assert ok, (mx, mr)
