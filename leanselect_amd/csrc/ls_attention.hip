@@ -6,7 +6,7 @@
 // keys are those of the valid ids in topk_idx[g, t, :] (each page once) with
 // j <= t + len_k - len_q when causal; all H/G heads of the group share the plan.
 //
-// Design (one wave per (token, group, 16-head tile)):
+// Design (one workgroup per 16 query rows of one KV group and 16-head tile):
 //   * the plan row is turned into an ascending, duplicate-free page list with
 //     an LDS bitmap (ids past the causal frontier are dropped);
 //   * S^T = K . Q^T on v_mfma_f32_16x16x32: keys are MFMA rows, the 16 heads of
@@ -23,7 +23,7 @@
 #include "ls_common.h"
 
 #define LS_ATTN_MAX_PAGES 8192
-#define LS_ATTN_MAX_TAKE 256
+#define LS_ATTN_MAX_TAKE 128
 
 __device__ __forceinline__ void ls_wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -43,16 +43,22 @@ __device__ __forceinline__ int ls_wave_excl_scan(int v, int lane, int* total) {
 }
 
 // pg_off[b] = sum_{b' < b} ceil(len_k(b') / 64): page-aligned start of each
-// sequence in the transposed V copy (in pages).
-__global__ void ls_attn_plan_kernel(const int32_t* __restrict__ cu_k, int batch,
-                                    int32_t* __restrict__ pg_off) {
+// sequence in the transposed V copy (in pages); tile_off[b] = sum_{b' < b}
+// ceil(len_q(b') / tile): first row tile of each sequence.
+__global__ void ls_attn_plan_kernel(const int32_t* __restrict__ cu_q,
+                                    const int32_t* __restrict__ cu_k, int batch, int tile,
+                                    int32_t* __restrict__ pg_off, int32_t* __restrict__ tile_off) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int32_t acc = 0;
+  int32_t acc = 0, acc_t = 0;
   pg_off[0] = 0;
+  tile_off[0] = 0;
   for (int b = 0; b < batch; ++b) {
     const int len = cu_k[b + 1] - cu_k[b];
     acc += len > 0 ? (len + 63) / 64 : 0;
     pg_off[b + 1] = acc;
+    const int lq = cu_q[b + 1] - cu_q[b];
+    acc_t += lq > 0 ? (lq + tile - 1) / tile : 0;
+    tile_off[b + 1] = acc_t;
   }
 }
 
@@ -113,171 +119,318 @@ __global__ __launch_bounds__(256) void ls_vt_kernel(const uint16_t* __restrict__
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tile kernel: one workgroup = 16 consecutive query rows of one sequence and
+// one KV group (8 waves x 2 rows).  The rows' page plans are OR-ed into a
+// sorted union page list; each union page of K and V^T is streamed once into
+// a 4-stage LDS ring with direct global->LDS loads issued three pages ahead,
+// and every row that selected the page runs its MFMAs on it.  Rows that did
+// not select a page skip it (no masked-out work).
+// ---------------------------------------------------------------------------
+#define LS_ATT_WAVES 8                       // waves per workgroup
+#define LS_ATT_TPW 2                         // rows per wave
+#define LS_ATT_TILE (LS_ATT_WAVES * LS_ATT_TPW)  // rows per workgroup
+#define LS_ATT_THREADS (64 * LS_ATT_WAVES)
+// 16-byte global->LDS copies per page issued by each wave: K is 64 rows of
+// 256 B (4 rows per copy), V^T 128 rows of 128 B (8 rows per copy).
+#define LS_ATT_K_COPIES (64 / LS_ATT_WAVES / 4)
+#define LS_ATT_V_COPIES (128 / LS_ATT_WAVES / 8)
+#define LS_ATT_COPIES (LS_ATT_K_COPIES + LS_ATT_V_COPIES)
+#define LS_ATT_STAGES 4
+#define LS_ATT_KBYTES (64 * 256)             // K page: 64 rows x 256 B
+#define LS_ATT_STAGE_BYTES (2 * LS_ATT_KBYTES)  // + V^T page: 128 rows x 128 B
+#define LS_ATT_WORDS (LS_ATTN_MAX_PAGES / 32)
+
+typedef __attribute__((address_space(3))) void ls_lds_void;
+
+// LDS row of key j (0..63) of a page: inside each 32-key chunk, MFMA row r of
+// key block nb holds key 8*(r/4) + 4*nb + r%4, so storing that key at row
+// 16*nb + r makes the 16 rows an MFMA reads consecutive, while lane group q
+// still ends up with the keys 8q..8q+7 of the chunk.
+__device__ __forceinline__ int ls_att_key_of_row(int row) {
+  const int c = row >> 5, rr = row & 31, nb = rr >> 4, r = rr & 15;
+  return 32 * c + 8 * (r >> 2) + 4 * nb + (r & 3);
+}
+
+// One 16-byte global->LDS load per lane (lane l lands at lds_off + 16 l; the
+// offset is wave-uniform).  Issued as inline asm so the compiler's wait
+// insertion does not treat every later LDS read as aliasing the in-flight
+// copy (which would drain the whole prefetch queue); the kernel orders the
+// copies itself with vmcnt waits and a barrier per page.
+__device__ __forceinline__ void ls_dma16(const void* gsrc, uint32_t lds_off) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(gsrc), "s"(lds_off)
+               : "memory", "m0");
+}
+
+// vmcnt(n) with the other counters left alone (gfx9 encoding).
+#define LS_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 0xf) | (((n) >> 4) << 14) | (0x7 << 4) | (0xf << 8))
+
 template <int DT>
-__global__ __launch_bounds__(256) void ls_attn_kernel(
+__global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
     const uint16_t* __restrict__ qg, int64_t q_rs, const uint16_t* __restrict__ kg,
     int64_t k_rs, const uint16_t* __restrict__ vt, int64_t lpad,
-    const int32_t* __restrict__ vexp, int64_t n_pages,
+    const int32_t* __restrict__ vexp, int64_t n_pages_ws,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
-    const int32_t* __restrict__ pg_off, int batch, int64_t total_q, int G, int gs,
-    const int32_t* __restrict__ topk_idx, int take, float scale_log2, int causal,
-    uint16_t* __restrict__ out, float* __restrict__ lse) {
+    const int32_t* __restrict__ pg_off, const int32_t* __restrict__ tile_off, int batch,
+    int64_t total_q, int G, int gs, const int32_t* __restrict__ topk_idx, int take,
+    float scale_log2, int causal, uint16_t* __restrict__ out, float* __restrict__ lse) {
   constexpr int D = 128;
-  __shared__ uint32_t s_bits[4][LS_ATTN_MAX_PAGES / 32];
-  __shared__ int32_t s_list[4][LS_ATTN_MAX_TAKE];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __shared__ __align__(16) uint8_t s_ring[LS_ATT_STAGES * LS_ATT_STAGE_BYTES];
+  __shared__ uint32_t s_bits[LS_ATT_TILE][LS_ATT_WORDS];
+  __shared__ uint16_t s_union[LS_ATT_TILE * LS_ATTN_MAX_TAKE];
+  __shared__ int8_t s_uexp[LS_ATT_TILE * LS_ATTN_MAX_TAKE];
+  __shared__ uint16_t s_umask[LS_ATT_TILE * LS_ATTN_MAX_TAKE];
+  __shared__ int s_wsum[LS_ATT_WAVES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int64_t t = (int64_t)blockIdx.x * 4 + w;
-  if (t >= total_q) return;
+
+  // XCD-aware tile order: consecutive workgroups land on different XCDs, so
+  // give each XCD a contiguous run of tiles (neighbouring rows share pages).
+  const int per_xcd = gridDim.x / 8;
+  const int64_t tile = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (tile >= tile_off[batch]) return;
   const int g = blockIdx.y;
-  const int head = blockIdx.z * 16 + r;  // head within the group
+  const int head = blockIdx.z * 16 + r;
   const bool head_ok = head < gs;
 
-  const int b = ls_find_segment(cu_q, batch, t);
-  const int64_t tr = t - cu_q[b];
+  const int b = ls_find_segment(tile_off, batch, tile);
+  const int64_t t0 = (int64_t)cu_q[b] + LS_ATT_TILE * (tile - tile_off[b]);
+  const int n_rows = (int)min((int64_t)LS_ATT_TILE, (int64_t)cu_q[b + 1] - t0);
   const int lq = cu_q[b + 1] - cu_q[b];
   const int lk = cu_k[b + 1] - cu_k[b];
   const int64_t kstart = cu_k[b];
   const int64_t vbase = 64LL * pg_off[b];
-  int64_t jmax = lk - 1;
-  if (causal) jmax = min(jmax, tr + (int64_t)(lk - lq));
+  const int64_t tr0 = t0 - cu_q[b];
+  // Keys visible to row i of the tile: j <= jmax(i) (the last row sees the most).
+  auto row_jmax = [&](int i) -> int64_t {
+    int64_t jm = lk - 1;
+    if (causal) jm = min(jm, tr0 + i + (int64_t)(lk - lq));
+    return jm;
+  };
+  const int64_t tile_jmax = row_jmax(n_rows - 1);
+  const int last_page =
+      tile_jmax >= 0 ? (int)min(tile_jmax / 64, (int64_t)LS_ATTN_MAX_PAGES - 1) : -1;
+  const int nwords = last_page / 32 + 1;
 
-  // ---- page list: ascending, unique, inside [0, jmax / 64] ----
-  int n_list = 0;
-  if (jmax >= 0) {
-    // The host bounds max_seqlen_k; the clamp keeps the LDS bitmap in range
-    // even when a caller understates it.
-    const int last_page = (int)min(jmax / 64, (int64_t)LS_ATTN_MAX_PAGES - 1);
-    const int nwords = last_page / 32 + 1;
-    uint32_t* bits = s_bits[w];
-    for (int i = lane; i < nwords; i += 64) bits[i] = 0u;
-    ls_wave_sync();
-    const int32_t* ids = topk_idx + ((int64_t)g * total_q + t) * take;
-    for (int i = lane; i < take; i += 64) {
+  // ---- per-row page bitmaps and their sorted union ----
+  for (int i = tid; i < LS_ATT_TILE * nwords; i += LS_ATT_THREADS) s_bits[i / nwords][i % nwords] = 0u;
+  __syncthreads();
+  if (last_page >= 0) {
+    const int32_t* ids = topk_idx + ((int64_t)g * total_q + t0) * take;
+    for (int i = tid; i < n_rows * take; i += LS_ATT_THREADS) {
+      const int row = i / take;
       const int p = ids[i];
-      if (p >= 0 && p <= last_page) atomicOr(&bits[p >> 5], 1u << (p & 31));
+      const int64_t jm = row_jmax(row);
+      if (p >= 0 && jm >= 0 && p <= jm / 64 && p <= last_page)
+        atomicOr(&s_bits[row][p >> 5], 1u << (p & 31));
     }
-    ls_wave_sync();
-    for (int w0 = 0; w0 < nwords; w0 += 64) {
-      const int i = w0 + lane;
-      uint32_t word = i < nwords ? bits[i] : 0u;
-      int tot;
-      int pos = n_list + ls_wave_excl_scan(__popc(word), lane, &tot);
-      while (word) {
-        const int bit = __ffs(word) - 1;
-        word &= word - 1;
-        s_list[w][pos++] = i * 32 + bit;
-      }
-      n_list += tot;
-    }
-    ls_wave_sync();
+  }
+  __syncthreads();
+  uint32_t word = 0u;
+  if (tid < nwords) {
+#pragma unroll
+    for (int i = 0; i < LS_ATT_TILE; ++i) word |= s_bits[i][tid];
+  }
+  int wtot;
+  const int wpos = ls_wave_excl_scan(__popc(word), lane, &wtot);
+  if (lane == 0) s_wsum[w] = wtot;
+  __syncthreads();
+  int pos = wpos;
+  for (int i = 0; i < w; ++i) pos += s_wsum[i];
+  int n_union = 0;
+#pragma unroll
+  for (int i = 0; i < LS_ATT_WAVES; ++i) n_union += s_wsum[i];
+  const int32_t* vexp_seq = vexp + (int64_t)g * n_pages_ws + pg_off[b];
+  const float inv_scale_log2 = 1.f / scale_log2;
+  while (word) {
+    const int bit = __ffs(word) - 1;
+    word &= word - 1;
+    const int page = tid * 32 + bit;
+    uint32_t rows = 0u;
+#pragma unroll
+    for (int i = 0; i < LS_ATT_TILE; ++i) rows |= ((s_bits[i][tid] >> bit) & 1u) << i;
+    s_uexp[pos] = (int8_t)vexp_seq[page];
+    s_umask[pos] = (uint16_t)rows;
+    s_union[pos++] = (uint16_t)page;
   }
 
-  // ---- Q^T fragments (B operand): head r, channels 32ks + 8q .. +7 ----
-  ls_u32x4 qf[4];
-  {
+  // ---- per-row state: Q^T fragments (B operand), softmax stats, O^T ----
+  ls_u32x4 qf[LS_ATT_TPW][4];
+  // m_run: running max in scaled base-2 units (score * scale_log2); thr: the
+  // raw score above which a key would exceed m_run by more than 2^8.
+  float m_run[LS_ATT_TPW], l_run[LS_ATT_TPW], thr[LS_ATT_TPW];
+  int jmax_r[LS_ATT_TPW];
+  ls_f32x4 o[LS_ATT_TPW][8];
+#pragma unroll
+  for (int j = 0; j < LS_ATT_TPW; ++j) {
+    const int row = w * LS_ATT_TPW + j;
+    const int64_t t = t0 + min(row, n_rows - 1);
     const uint16_t* qrow = qg + t * q_rs + ((int64_t)g * gs + (head_ok ? head : 0)) * D + 8 * q;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      qf[ks] = ls_load16(qrow + 32 * ks);
-      if (!head_ok) qf[ks] = ls_u32x4{0u, 0u, 0u, 0u};
+      qf[j][ks] = ls_load16(qrow + 32 * ks);
+      if (!head_ok) qf[j][ks] = ls_u32x4{0u, 0u, 0u, 0u};
     }
-  }
-
-  float m_run = -INFINITY, l_run = 0.f;
-  ls_f32x4 o[8];
+    m_run[j] = -INFINITY;
+    l_run[j] = 0.f;
+    thr[j] = -INFINITY;
+    jmax_r[j] = row < n_rows ? (int)row_jmax(row) : -1;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int db = 0; db < 8; ++db) o[j][db] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  __syncthreads();  // union list, exponents and every wave's Q loads are complete
+  LS_WAIT_VMCNT(0);
 
-  const uint16_t* kgrp = kg + (int64_t)g * D + 8 * q;
-  const uint16_t* vgrp = vt + ((int64_t)g * D + r) * lpad + vbase + 8 * q;
-  // Row of the K fragment for MFMA row r: keys base + 8(r/4) + 4nb + r%4.
-  const int krow_off = 8 * (r >> 2) + (r & 3);
+  // ---- staging: wave w moves K rows 4*K_COPIES*w.. and V^T rows 8*V_COPIES*w.. ----
+  // K row R holds key ls_att_key_of_row(R) with its 16-byte chunk C stored at
+  // position C ^ (R & 7); V^T row d likewise with position C ^ (d & 7).  Each
+  // instruction fills 1 KB of contiguous LDS (lane l -> byte 16 l).
+  const uint16_t* kgrp = kg + (int64_t)g * D;
+  const uint16_t* vgrp = vt + (int64_t)g * D * lpad + vbase;
+  const uint32_t ring_off = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(ls_lds_void*)s_ring);
+  auto issue = [&](int page, int stage) {
+    const uint32_t kb = ring_off + stage * LS_ATT_STAGE_BYTES;
+    const uint32_t vb = kb + LS_ATT_KBYTES;
+#pragma unroll
+    for (int i = 0; i < LS_ATT_K_COPIES; ++i) {
+      const int R0 = 4 * (LS_ATT_K_COPIES * w + i);
+      const int R = R0 + (lane >> 4);
+      const int C = (lane & 15) ^ (R & 7);
+      const int64_t kr = min((int64_t)64 * page + ls_att_key_of_row(R), (int64_t)lk - 1);
+      ls_dma16(kgrp + (kstart + kr) * k_rs + 8 * C, __builtin_amdgcn_readfirstlane(kb + R0 * 256));
+    }
+#pragma unroll
+    for (int i = 0; i < LS_ATT_V_COPIES; ++i) {
+      const int d0 = 8 * (LS_ATT_V_COPIES * w + i);
+      const int d = d0 + (lane >> 3);
+      const int C = (lane & 7) ^ (d & 7);
+      ls_dma16(vgrp + (int64_t)d * lpad + 64LL * page + 8 * C,
+               __builtin_amdgcn_readfirstlane(vb + d0 * 128));
+    }
+  };
 
-  const int32_t* vexp_seq = vexp + (int64_t)g * n_pages + pg_off[b];
-  for (int pi = 0; pi < n_list; ++pi) {
-    const int page = s_list[w][pi];
-    const float p_scale = __builtin_ldexpf(1.f, vexp_seq[page]);
+#pragma unroll
+  for (int sidx = 0; sidx < LS_ATT_STAGES - 1; ++sidx)
+    if (sidx < n_union) issue(s_union[sidx], sidx);
+
+  for (int ui = 0; ui < n_union; ++ui) {
+    // Pages issued after page ui by this wave: min(STAGES - 2, n_union - 1 - ui).
+    const int pending = min(LS_ATT_STAGES - 2, n_union - 1 - ui);
+    if (pending >= 2) LS_WAIT_VMCNT(2 * LS_ATT_COPIES);
+    else if (pending == 1) LS_WAIT_VMCNT(LS_ATT_COPIES);
+    else LS_WAIT_VMCNT(0);
+    __syncthreads();  // page ui is in LDS for everyone; stage (ui - 1) % STAGES is free
+    if (ui + LS_ATT_STAGES - 1 < n_union)
+      issue(s_union[ui + LS_ATT_STAGES - 1], (ui + LS_ATT_STAGES - 1) % LS_ATT_STAGES);
+
+    const int page = s_union[ui];
+    const int sel = __builtin_amdgcn_readfirstlane(
+        (s_umask[ui] >> (LS_ATT_TPW * w)) & ((1 << LS_ATT_TPW) - 1));
+    if (!sel) continue;
+    const int v_e = s_uexp[ui];
+    const float p_scale = __builtin_ldexpf(1.f, v_e);
+    const uint8_t* kb = s_ring + (ui % LS_ATT_STAGES) * LS_ATT_STAGE_BYTES;
+    const uint8_t* vb = kb + LS_ATT_KBYTES;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const int64_t base = 64LL * page + 32 * c;
-      if (base > jmax) break;
-      ls_u32x4 kf0[4], kf1[4];
-      {
-        const int64_t k0 = min(base + krow_off, (int64_t)lk - 1);
-        const int64_t k1 = min(base + krow_off + 4, (int64_t)lk - 1);
-        const uint16_t* p0 = kgrp + (kstart + k0) * k_rs;
-        const uint16_t* p1 = kgrp + (kstart + k1) * k_rs;
+      const int base = 64 * page + 32 * c;
+      int need = 0;
+#pragma unroll
+      for (int j = 0; j < LS_ATT_TPW; ++j) need |= (((sel >> j) & 1) && base <= jmax_r[j]) << j;
+      need = __builtin_amdgcn_readfirstlane(need);
+      if (!need) continue;
+      // Fragment addresses; the fragments are read from LDS per row (most
+      // pages serve one or two rows of a wave), which keeps register pressure
+      // low enough for the accumulators to stay put.
+      const int R0 = 32 * c + r, R1 = 32 * c + 16 + r;
+      const uint8_t* k0p = kb + R0 * 256;
+      const uint8_t* k1p = kb + R1 * 256;
+      const uint8_t* vrow = vb + r * 128;
+      const int key0 = base + 8 * q;
+#pragma unroll
+      for (int j = 0; j < LS_ATT_TPW; ++j) {
+        if (!((need >> j) & 1)) continue;
+        ls_f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          kf0[ks] = ls_load16(p0 + 32 * ks);
-          kf1[ks] = ls_load16(p1 + 32 * ks);
+          const int C = 4 * ks + q;
+          const ls_u32x4 kf0 = *reinterpret_cast<const ls_u32x4*>(k0p + ((C ^ (R0 & 7)) << 4));
+          const ls_u32x4 kf1 = *reinterpret_cast<const ls_u32x4*>(k1p + ((C ^ (R1 & 7)) << 4));
+          s0 = LsElem<DT>::mfma(kf0, qf[j][ks], s0);
+          s1 = LsElem<DT>::mfma(kf1, qf[j][ks], s1);
         }
-      }
-      ls_u32x4 vf[8];
+        // Lane (r, q) holds head r's raw scores of keys base + 8q + 0..7.
+        float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+        if (base + 31 > jmax_r[j]) {  // the chunk crosses this row's causal frontier
 #pragma unroll
-      for (int db = 0; db < 8; ++db) vf[db] = ls_load16(vgrp + (int64_t)16 * db * lpad + base);
-
-      ls_f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+          for (int i = 0; i < 8; ++i)
+            if (key0 + i > jmax_r[j]) sv[i] = -INFINITY;
+        }
+        const float lmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                                 fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+        // Rescale only when some head's max grows by more than 2^8 (or when the
+        // page's V scale leaves too little fp16 headroom for P up to 2^8).
+        if (__ballot(lmax > thr[j]) != 0ull || v_e > 7) {
+          float cm = lmax;
+          cm = fmaxf(cm, ls_shfl_xor(cm, 16));
+          cm = fmaxf(cm, ls_shfl_xor(cm, 32));
+          const float m_new = fmaxf(m_run[j], cm * scale_log2);
+          const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
+          m_run[j] = m_new;
+          thr[j] = (m_new + 8.f) * inv_scale_log2;
+          l_run[j] *= alpha;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        s0 = LsElem<DT>::mfma(kf0[ks], qf[ks], s0);
-        s1 = LsElem<DT>::mfma(kf1[ks], qf[ks], s1);
-      }
-      // Lane (r, q) now holds head r's scores of keys base + 8q + 0..7.
-      float sv[8];
+          for (int db = 0; db < 8; ++db) o[j][db] *= alpha;
+        }
+        const float neg_m = -m_run[j];
+        float pv[8], lsum = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sv[i] = s0[i] * scale_log2;
-        sv[4 + i] = s1[i] * scale_log2;
-      }
-      const int64_t key0 = base + 8 * q;
+        for (int i = 0; i < 8; ++i) {
+          pv[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], scale_log2, neg_m));
+          lsum += pv[i];
+        }
+        l_run[j] += lsum;
+        // P . V on the fp16 MFMA; the page's V scale moves onto P exactly.
+        ls_u32x4 pf;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (key0 + i > jmax) sv[i] = -INFINITY;
-      float cm = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                       fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-      cm = fmaxf(cm, ls_shfl_xor(cm, 16));
-      cm = fmaxf(cm, ls_shfl_xor(cm, 32));
-      const float m_new = fmaxf(m_run, cm);
-      if (m_new == -INFINITY) continue;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      float pv[8], lsum = 0.f;
+        for (int i = 0; i < 4; ++i)
+          pf[i] = ls_pack2(ls_f32_to_f16(pv[2 * i] * p_scale), ls_f32_to_f16(pv[2 * i + 1] * p_scale));
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        pv[i] = __builtin_amdgcn_exp2f(sv[i] - m_new);
-        lsum += pv[i];
-      }
-      l_run = l_run * alpha + lsum;
-      m_run = m_new;
-      // P * V on the fp16 MFMA: P in [0, 1] keeps 10 mantissa bits; the page's
-      // power-of-two V scale moves onto P exactly.
-      ls_u32x4 pf;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        pf[i] = ls_pack2(ls_f32_to_f16(pv[2 * i] * p_scale), ls_f32_to_f16(pv[2 * i + 1] * p_scale));
-#pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        o[db] *= alpha;
-        o[db] = LsElem<LS_F16>::mfma(vf[db], pf, o[db]);
+        for (int db = 0; db < 8; ++db) {
+          // V^T row 16 db + r (so row & 7 == r & 7), logical chunk 4c + q.
+          const ls_u32x4 vf = *reinterpret_cast<const ls_u32x4*>(
+              vrow + db * 2048 + (((4 * c + q) ^ (r & 7)) << 4));
+          o[j][db] = LsElem<LS_F16>::mfma(vf, pf, o[j][db]);
+        }
       }
     }
   }
 
-  float l_tot = l_run + ls_shfl_xor(l_run, 16);
-  l_tot += ls_shfl_xor(l_tot, 32);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (head_ok) {
+  // ---- epilogue ----
+#pragma unroll
+  for (int j = 0; j < LS_ATT_TPW; ++j) {
+    const int row = w * LS_ATT_TPW + j;
+    float l_tot = l_run[j] + ls_shfl_xor(l_run[j], 16);
+    l_tot += ls_shfl_xor(l_tot, 32);
+    if (row >= n_rows || !head_ok) continue;
+    const int64_t t = t0 + row;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     uint16_t* orow = out + (t * G * gs + (int64_t)g * gs + head) * D + 4 * q;
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
-      uint32_t lo = ls_pack2(LsElem<DT>::from_f(o[db][0] * inv), LsElem<DT>::from_f(o[db][1] * inv));
-      uint32_t hi = ls_pack2(LsElem<DT>::from_f(o[db][2] * inv), LsElem<DT>::from_f(o[db][3] * inv));
+      const uint32_t lo = ls_pack2(LsElem<DT>::from_f(o[j][db][0] * inv), LsElem<DT>::from_f(o[j][db][1] * inv));
+      const uint32_t hi = ls_pack2(LsElem<DT>::from_f(o[j][db][2] * inv), LsElem<DT>::from_f(o[j][db][3] * inv));
       *reinterpret_cast<uint2*>(orow + 16 * db) = make_uint2(lo, hi);
     }
     if (lse && q == 0)
       lse[((int64_t)g * gs + head) * total_q + t] =
-          l_tot > 0.f ? m_run * 0.69314718055994531f + __logf(l_tot) : INFINITY;
+          l_tot > 0.f ? m_run[j] * 0.69314718055994531f + __logf(l_tot) : INFINITY;
   }
 }
 
@@ -286,7 +439,7 @@ __global__ __launch_bounds__(256) void ls_attn_kernel(
 // ---------------------------------------------------------------------------
 namespace {
 struct AttnWs {
-  size_t vt, pg, vexp, total;
+  size_t vt, pg, tiles, vexp, total;
   int64_t lpad, n_pages;
 };
 AttnWs attn_ws(int64_t total_k, int batch, int G, int D, int eb) {
@@ -296,6 +449,7 @@ AttnWs attn_ws(int64_t total_k, int batch, int G, int D, int eb) {
   size_t off = 0;
   L.vt = off; off += ls_align256((size_t)G * D * L.lpad * eb);
   L.pg = off; off += ls_align256((size_t)(batch + 1) * 4);
+  L.tiles = off; off += ls_align256((size_t)(batch + 1) * 4);
   L.vexp = off; off += ls_align256((size_t)G * L.n_pages * 4);
   L.total = off;
   return L;
@@ -349,7 +503,9 @@ extern "C" int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const 
   uint16_t* vt = (uint16_t*)(ws + L.vt);
   int32_t* pg = (int32_t*)(ws + L.pg);
   int32_t* vexp = (int32_t*)(ws + L.vexp);
-  hipLaunchKernelGGL(ls_attn_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens_k, batch, pg);
+  int32_t* tiles = (int32_t*)(ws + L.tiles);
+  hipLaunchKernelGGL(ls_attn_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens_q, cu_seqlens_k,
+                     batch, LS_ATT_TILE, pg, tiles);
   int rc = ls_check_launch("ls_attn_plan_kernel");
   if (rc) return rc;
   if (total_k > 0) {
@@ -365,16 +521,17 @@ extern "C" int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const 
   const int gs = num_heads / num_kv_heads;
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf((float)head_dim);
   const float scale_log2 = scale * 1.4426950408889634f;
-  const dim3 grid((unsigned)((total_q + 3) / 4), num_kv_heads, (gs + 15) / 16);
+  const int64_t tile_bound = (total_q + LS_ATT_TILE - 1) / LS_ATT_TILE + batch;
+  const dim3 grid((unsigned)(8 * ((tile_bound + 7) / 8)), num_kv_heads, (gs + 15) / 16);
   if (dtype == LS_BF16)
-    hipLaunchKernelGGL(ls_attn_kernel<LS_BF16>, grid, dim3(256), 0, s, (const uint16_t*)q,
-                       q_row_stride, (const uint16_t*)k, k_row_stride, vt, L.lpad, vexp, L.n_pages, cu_seqlens_q,
-                       cu_seqlens_k, pg, batch, total_q, num_kv_heads, gs, topk_idx, take,
-                       scale_log2, causal, (uint16_t*)out, lse);
+    hipLaunchKernelGGL(ls_attn_tile_kernel<LS_BF16>, grid, dim3(LS_ATT_THREADS), 0, s, (const uint16_t*)q,
+                       q_row_stride, (const uint16_t*)k, k_row_stride, vt, L.lpad, vexp,
+                       L.n_pages, cu_seqlens_q, cu_seqlens_k, pg, tiles, batch, total_q,
+                       num_kv_heads, gs, topk_idx, take, scale_log2, causal, (uint16_t*)out, lse);
   else
-    hipLaunchKernelGGL(ls_attn_kernel<LS_F16>, grid, dim3(256), 0, s, (const uint16_t*)q,
-                       q_row_stride, (const uint16_t*)k, k_row_stride, vt, L.lpad, vexp, L.n_pages, cu_seqlens_q,
-                       cu_seqlens_k, pg, batch, total_q, num_kv_heads, gs, topk_idx, take,
-                       scale_log2, causal, (uint16_t*)out, lse);
-  return ls_check_launch("ls_attn_kernel");
+    hipLaunchKernelGGL(ls_attn_tile_kernel<LS_F16>, grid, dim3(LS_ATT_THREADS), 0, s, (const uint16_t*)q,
+                       q_row_stride, (const uint16_t*)k, k_row_stride, vt, L.lpad, vexp,
+                       L.n_pages, cu_seqlens_q, cu_seqlens_k, pg, tiles, batch, total_q,
+                       num_kv_heads, gs, topk_idx, take, scale_log2, causal, (uint16_t*)out, lse);
+  return ls_check_launch("ls_attn_tile_kernel");
 }
