@@ -127,7 +127,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="minicpm41_8b_layer_128k", choices=sorted(WORKLOADS))
     ap.add_argument("--kernel-iters", type=int, default=5)
-    ap.add_argument("--cpu-rows-per-seq", type=int, default=256)
+    ap.add_argument("--cpu-rows-per-seq", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:

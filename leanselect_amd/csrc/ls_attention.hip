@@ -164,6 +164,14 @@ __device__ __forceinline__ void ls_dma16(const void* gsrc, uint32_t lds_off) {
                : "memory", "m0");
 }
 
+// max of three floats in one instruction (inputs are finite or -inf scores, so
+// the NaN quieting that fmaxf would add is not needed).
+__device__ __forceinline__ float ls_max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // vmcnt(n) with the other counters left alone (gfx9 encoding).
 #define LS_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt(((n) & 0xf) | (((n) >> 4) << 14) | (0x7 << 4) | (0xf << 8))
@@ -288,8 +296,9 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
 
   // ---- staging: wave w moves K rows 4*K_COPIES*w.. and V^T rows 8*V_COPIES*w.. ----
   // K row R holds key ls_att_key_of_row(R) with its 16-byte chunk C stored at
-  // position C ^ (R & 7); V^T row d likewise with position C ^ (d & 7).  Each
-  // instruction fills 1 KB of contiguous LDS (lane l -> byte 16 l).
+  // position C ^ (R & 15); V^T row d (8 chunks) at position C ^ ((d >> 1) & 7).
+  // The sixteen lanes of an MFMA operand read then hit sixteen distinct bank
+  // groups.  Each copy fills 1 KB of contiguous LDS (lane l -> byte 16 l).
   const uint16_t* kgrp = kg + (int64_t)g * D;
   const uint16_t* vgrp = vt + (int64_t)g * D * lpad + vbase;
   const uint32_t ring_off = __builtin_amdgcn_readfirstlane(
@@ -301,7 +310,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
     for (int i = 0; i < LS_ATT_K_COPIES; ++i) {
       const int R0 = 4 * (LS_ATT_K_COPIES * w + i);
       const int R = R0 + (lane >> 4);
-      const int C = (lane & 15) ^ (R & 7);
+      const int C = (lane & 15) ^ (R & 15);
       const int64_t kr = min((int64_t)64 * page + ls_att_key_of_row(R), (int64_t)lk - 1);
       ls_dma16(kgrp + (kstart + kr) * k_rs + 8 * C, __builtin_amdgcn_readfirstlane(kb + R0 * 256));
     }
@@ -309,7 +318,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
     for (int i = 0; i < LS_ATT_V_COPIES; ++i) {
       const int d0 = 8 * (LS_ATT_V_COPIES * w + i);
       const int d = d0 + (lane >> 3);
-      const int C = (lane & 7) ^ (d & 7);
+      const int C = (lane & 7) ^ ((d >> 1) & 7);
       ls_dma16(vgrp + (int64_t)d * lpad + 64LL * page + 8 * C,
                __builtin_amdgcn_readfirstlane(vb + d0 * 128));
     }
@@ -334,7 +343,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
         (s_umask[ui] >> (LS_ATT_TPW * w)) & ((1 << LS_ATT_TPW) - 1));
     if (!sel) continue;
     const int v_e = s_uexp[ui];
-    const float p_scale = __builtin_ldexpf(1.f, v_e);
+    const float p_unscale = __builtin_ldexpf(1.f, -v_e);
     const uint8_t* kb = s_ring + (ui % LS_ATT_STAGES) * LS_ATT_STAGE_BYTES;
     const uint8_t* vb = kb + LS_ATT_KBYTES;
 #pragma unroll
@@ -345,13 +354,19 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
       for (int j = 0; j < LS_ATT_TPW; ++j) need |= (((sel >> j) & 1) && base <= jmax_r[j]) << j;
       need = __builtin_amdgcn_readfirstlane(need);
       if (!need) continue;
-      // Fragment addresses; the fragments are read from LDS per row (most
-      // pages serve one or two rows of a wave), which keeps register pressure
-      // low enough for the accumulators to stay put.
+      // The chunk's K and V^T fragments are read once and shared by the rows.
       const int R0 = 32 * c + r, R1 = 32 * c + 16 + r;
-      const uint8_t* k0p = kb + R0 * 256;
-      const uint8_t* k1p = kb + R1 * 256;
-      const uint8_t* vrow = vb + r * 128;
+      ls_u32x4 kf0[4], kf1[4], vf[8];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int C = 4 * ks + q;
+        kf0[ks] = *reinterpret_cast<const ls_u32x4*>(kb + R0 * 256 + ((C ^ (R0 & 15)) << 4));
+        kf1[ks] = *reinterpret_cast<const ls_u32x4*>(kb + R1 * 256 + ((C ^ (R1 & 15)) << 4));
+      }
+      // V^T row 16 db + r (so (row >> 1) & 7 == (r >> 1) & 7), logical chunk 4c + q.
+      const uint8_t* vrow = vb + r * 128 + (((4 * c + q) ^ ((r >> 1) & 7)) << 4);
+#pragma unroll
+      for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
       const int key0 = base + 8 * q;
 #pragma unroll
       for (int j = 0; j < LS_ATT_TPW; ++j) {
@@ -359,11 +374,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
         ls_f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const int C = 4 * ks + q;
-          const ls_u32x4 kf0 = *reinterpret_cast<const ls_u32x4*>(k0p + ((C ^ (R0 & 7)) << 4));
-          const ls_u32x4 kf1 = *reinterpret_cast<const ls_u32x4*>(k1p + ((C ^ (R1 & 7)) << 4));
-          s0 = LsElem<DT>::mfma(kf0, qf[j][ks], s0);
-          s1 = LsElem<DT>::mfma(kf1, qf[j][ks], s1);
+          s0 = LsElem<DT>::mfma(kf0[ks], qf[j][ks], s0);
+          s1 = LsElem<DT>::mfma(kf1[ks], qf[j][ks], s1);
         }
         // Lane (r, q) holds head r's raw scores of keys base + 8q + 0..7.
         float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
@@ -372,8 +384,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
           for (int i = 0; i < 8; ++i)
             if (key0 + i > jmax_r[j]) sv[i] = -INFINITY;
         }
-        const float lmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                                 fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+        const float lmax = fmaxf(ls_max3(sv[0], sv[1], sv[2]),
+                                 ls_max3(ls_max3(sv[3], sv[4], sv[5]), sv[6], sv[7]));
         // Rescale only when some head's max grows by more than 2^8 (or when the
         // page's V scale leaves too little fp16 headroom for P up to 2^8).
         if (__ballot(lmax > thr[j]) != 0ull || v_e > 7) {
@@ -388,26 +400,20 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
 #pragma unroll
           for (int db = 0; db < 8; ++db) o[j][db] *= alpha;
         }
-        const float neg_m = -m_run[j];
+        // P' = P * 2^e (the page's V scale moved onto P, exact): one exp each.
+        const float bias = (float)v_e - m_run[j];
         float pv[8], lsum = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          pv[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], scale_log2, neg_m));
+          pv[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], scale_log2, bias));
           lsum += pv[i];
         }
-        l_run[j] += lsum;
-        // P . V on the fp16 MFMA; the page's V scale moves onto P exactly.
+        l_run[j] += v_e ? lsum * p_unscale : lsum;
         ls_u32x4 pf;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          pf[i] = ls_pack2(ls_f32_to_f16(pv[2 * i] * p_scale), ls_f32_to_f16(pv[2 * i + 1] * p_scale));
+        for (int i = 0; i < 4; ++i) pf[i] = ls_pack2(ls_f32_to_f16(pv[2 * i]), ls_f32_to_f16(pv[2 * i + 1]));
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-          // V^T row 16 db + r (so row & 7 == r & 7), logical chunk 4c + q.
-          const ls_u32x4 vf = *reinterpret_cast<const ls_u32x4*>(
-              vrow + db * 2048 + (((4 * c + q) ^ (r & 7)) << 4));
-          o[j][db] = LsElem<LS_F16>::mfma(vf, pf, o[j][db]);
-        }
+        for (int db = 0; db < 8; ++db) o[j][db] = LsElem<LS_F16>::mfma(vf[db], pf, o[j][db]);
       }
     }
   }
