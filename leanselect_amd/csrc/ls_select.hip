@@ -104,6 +104,102 @@ __global__ __launch_bounds__(256) void ls_proj_mfma_kernel(
   }
 }
 
+// Projection GEMM for long A (the q~ projection streams every query row once):
+// a workgroup owns 128 rows x F columns, the weight tile of each 128-wide K
+// step is staged once in LDS (double buffered, 16-byte chunks XOR-swizzled by
+// column) and shared by the four waves, and each wave prefetches its next A
+// step while the MFMAs of the current one run.  The reduction index is
+// permuted inside a K step: lane group q takes k = 32q + 8ks .. +7 in slice
+// ks, for both operands, so every lane reads 64 contiguous bytes of its A row.
+// Requires K % 128 == 0.
+template <int DT, int FB>
+__global__ __launch_bounds__(256, 2) void ls_proj_tile_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, int64_t gk, int64_t M, int K,
+    const uint16_t* __restrict__ wt, uint16_t* __restrict__ out) {
+  constexpr int F = FB * 16;
+  constexpr int NB = F * 16 / 256;  // 16-byte weight chunks per thread per K step
+  __shared__ ls_u32x4 sB[2][F * 16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int g = blockIdx.y;
+  const int64_t m0 = (int64_t)blockIdx.x * 128 + w * 32;
+  const uint16_t* Ag = A + g * gk;
+  const uint16_t* Wg = wt + (int64_t)g * F * K;
+  const uint16_t* a0p = Ag + min(m0 + r, M - 1) * lda + 32 * q;
+  const uint16_t* a1p = Ag + min(m0 + 16 + r, M - 1) * lda + 32 * q;
+  const int nk = K / 128;
+
+  ls_u32x4 breg[NB];
+  auto load_b = [&](int kt) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int i = tid + 256 * j, f = i >> 4, ch = i & 15;
+      breg[j] = ls_load16(Wg + (int64_t)f * K + 128 * kt + 8 * ch);
+    }
+  };
+  auto store_b = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int i = tid + 256 * j, f = i >> 4, ch = i & 15;
+      sB[buf][f * 16 + (ch ^ (f & 15))] = breg[j];
+    }
+  };
+  ls_u32x4 a0[4], a1[4];
+  auto load_a = [&](int kt) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      a0[ks] = ls_load16(a0p + 128 * kt + 8 * ks);
+      a1[ks] = ls_load16(a1p + 128 * kt + 8 * ks);
+    }
+  };
+
+  ls_f32x4 acc0[FB], acc1[FB];
+#pragma unroll
+  for (int c = 0; c < FB; ++c) {
+    acc0[c] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
+    acc1[c] = acc0[c];
+  }
+  load_b(0);
+  load_a(0);
+  store_b(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    ls_u32x4 c0[4], c1[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      c0[ks] = a0[ks];
+      c1[ks] = a1[ks];
+    }
+    if (kt + 1 < nk) {
+      load_b(kt + 1);
+      load_a(kt + 1);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int c = 0; c < FB; ++c) {
+        const ls_u32x4 b = sB[buf][(16 * c + r) * 16 + ((4 * q + ks) ^ r)];
+        acc0[c] = LsElem<DT>::mfma(c0[ks], b, acc0[c]);
+        acc1[c] = LsElem<DT>::mfma(c1[ks], b, acc1[c]);
+      }
+    }
+    if (kt + 1 < nk) store_b(buf ^ 1);
+    __syncthreads();
+  }
+  if (m0 >= M) return;
+  uint16_t* og = out + (int64_t)g * M * F;
+#pragma unroll
+  for (int c = 0; c < FB; ++c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t ma = m0 + 4 * q + i, mb = m0 + 16 + 4 * q + i;
+      if (ma < M) og[ma * F + c * 16 + r] = LsElem<DT>::from_f(acc0[c][i]);
+      if (mb < M) og[mb * F + c * 16 + r] = LsElem<DT>::from_f(acc1[c][i]);
+    }
+  }
+}
+
 // float32 projection on the vector ALU (the reference's float32 path).
 __global__ __launch_bounds__(256) void ls_proj_f32_kernel(
     const float* __restrict__ A, int64_t lda, int64_t gk, int64_t M, int K, int F,
@@ -137,11 +233,14 @@ __global__ void ls_select_plan_kernel(const int32_t* __restrict__ cu_q, int batc
 
 // ---------------------------------------------------------------------------
 // Page scores on MFMA.  One workgroup = one 64-token query block of one KV
-// group; wave w owns tokens 16w..16w+15.  Atoms are the MFMA rows, tokens the
-// columns, so after one 16-atom step lane l (q = l/16) holds the four atoms
-// 16j+4q..16j+4q+3 of page 4j+q for token l%16; the fifth atom of the window
-// (16j+4q-1) is the last atom of the lane group below, one rotate away, or
-// the carry from the previous step for q == 0.
+// group; the block's atom range is split into four contiguous quarters, one
+// per wave, and every wave scores all 64 tokens (four 16-token MFMA column
+// blocks), so each k~ fragment is read once per workgroup and feeds four
+// MFMAs.  Atoms are the MFMA rows and tokens the columns: after one 16-atom
+// step lane l (q = l/16) holds the four atoms 16j+4q..16j+4q+3 of page 4j+q
+// for token l%16; the fifth atom of the window (16j+4q-1) is the last atom of
+// the lane group below, one rotate away, or the carry from the previous step
+// for q == 0.
 //
 // SELECT: per sequence, only the non-forced visible pages
 // [init_blocks, qp - local_blocks - 1] of the block are scored, into the
@@ -154,7 +253,7 @@ __global__ __launch_bounds__(256) void ls_score_mfma_kernel(
     const int32_t* __restrict__ blk_off, int batch, int64_t n_blk_launch, int init_blocks,
     int local_blocks, int64_t full_seq_len, uint16_t* __restrict__ out, int64_t out_stride) {
   constexpr int F = KS * 32;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int g = blockIdx.y;
 
@@ -180,37 +279,68 @@ __global__ __launch_bounds__(256) void ls_score_mfma_kernel(
     p_hi = (int)((full_seq_len + 63) / 64) - 1;
   }
   if (n_atoms <= 0 || p_lo > p_hi) return;
-  const int64_t wt0 = tq0 + 16 * w;
-  if (wt0 >= tq_end) return;
-  const int64_t tok = min(wt0 + r, tq_end - 1);
-  const bool tok_ok = wt0 + r < tq_end;
 
-  ls_u32x4 qf[KS];
-  const uint16_t* qrow = qt + ((int64_t)g * Nq + tok) * F + 8 * q;
+  // This wave's share of the block's 16-atom steps.
+  const int j_lo = p_lo >> 2, j_hi = p_hi >> 2;
+  const int n_j = j_hi - j_lo + 1;
+  const int jw_lo = j_lo + (n_j * w) / 4, jw_hi = j_lo + (n_j * (w + 1)) / 4 - 1;
+  if (jw_lo > jw_hi) return;
+
+  // q~^T fragments (B operand) of the four 16-token column blocks.
+  ls_u32x4 qf[4][KS];
+  bool tok_ok[4];
+  int64_t tok[4];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) qf[ks] = ls_load16(qrow + 32 * ks);
+  for (int tb = 0; tb < 4; ++tb) {
+    tok_ok[tb] = tq0 + 16 * tb + r < tq_end;
+    tok[tb] = min(tq0 + 16 * tb + r, tq_end - 1);
+    const uint16_t* qrow = qt + ((int64_t)g * Nq + tok[tb]) * F + 8 * q;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[tb][ks] = ls_load16(qrow + 32 * ks);
+  }
 
   const uint16_t* kbase = kt + ((int64_t)g * Na + a0) * F + 8 * q;
-  uint16_t* orow = out + ((int64_t)g * Nq + tok) * out_stride;
-  const int j_lo = p_lo >> 2, j_hi = p_hi >> 2;
-  float carry = -INFINITY;
-  for (int j = (j_lo > 0 ? j_lo - 1 : 0); j <= j_hi; ++j) {
-    const int64_t arow = min((int64_t)16 * j + r, n_atoms - 1);
-    const uint16_t* kp = kbase + arow * F;
-    ls_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float carry[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  const int j_first = jw_lo > 0 ? jw_lo - 1 : 0;  // one step early primes the carry
+  ls_u32x4 kf[KS];
+  {
+    const uint16_t* kp = kbase + min((int64_t)16 * j_first + r, n_atoms - 1) * F;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) acc = LsElem<DT>::mfma(ls_load16(kp + 32 * ks), qf[ks], acc);
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = ls_load16(kp + 32 * ks);
+  }
+  for (int j = j_first; j <= jw_hi; ++j) {
+    ls_u32x4 kn[KS];
+    if (j < jw_hi) {  // prefetch the next step's k~ rows
+      const uint16_t* kp = kbase + min((int64_t)16 * (j + 1) + r, n_atoms - 1) * F;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kn[ks] = ls_load16(kp + 32 * ks);
+    }
+    ls_f32x4 acc[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      acc[tb] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) acc[tb] = LsElem<DT>::mfma(kf[ks], qf[tb][ks], acc[tb]);
+    }
     const int64_t atom0 = (int64_t)16 * j + 4 * q;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (atom0 + i >= n_atoms) acc[i] = -INFINITY;
-    const float m4 = fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3]));
-    const float rot = ls_shfl(acc[3], (lane - 16) & 63);
-    const float prev = q == 0 ? carry : rot;
-    carry = rot;
     const int p = 4 * j + q;
-    if (j >= j_lo && p >= p_lo && p <= p_hi && tok_ok)
-      orow[p] = LsElem<DT>::from_f(fmaxf(m4, prev));
+    const bool write = j >= jw_lo && p >= p_lo && p <= p_hi;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (atom0 + i >= n_atoms) acc[tb][i] = -INFINITY;
+      const float m4 = fmaxf(fmaxf(acc[tb][0], acc[tb][1]), fmaxf(acc[tb][2], acc[tb][3]));
+      const float rot = ls_shfl(acc[tb][3], (lane - 16) & 63);
+      const float prev = q == 0 ? carry[tb] : rot;
+      carry[tb] = rot;
+      if (write && tok_ok[tb])
+        out[((int64_t)g * Nq + tok[tb]) * out_stride + p] = LsElem<DT>::from_f(fmaxf(m4, prev));
+    }
+    if (j < jw_hi) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = kn[ks];
+    }
   }
 }
 
@@ -266,10 +396,65 @@ __device__ __forceinline__ uint32_t ls_order_key32(uint32_t u) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ int ls_wave_sum(int v) {
+// Number of set bits of `mask` in the lanes below this one.
+__device__ __forceinline__ int ls_lanes_below(uint64_t mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// Top-kk of one row's cn candidate scores (columns base .. base + cn - 1 of
+// P), held as order-preserving keys in NS register slots of 64 lanes.  Loads
+// are issued together (addresses clamped into the row), then converted; keys
+// of lanes past cn are 0, which no threshold candidate (>= 1) counts.  The
+// kk-th largest key T is found by bisection over the key bits with ballot
+// counts; the winners (key > T, then the first kk - #{key > T} keys equal to
+// T in page order) are written in page order after the lo_end sink pages.
+template <int NS, bool KEY32>
+__device__ __forceinline__ void ls_topk_row(const void* __restrict__ P, int64_t base, int cn,
+                                            int kk, int lo_end, int lane,
+                                            int32_t* __restrict__ orow) {
+  uint32_t key[NS];
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, LS_WAVE);
-  return v;
+  for (int s = 0; s < NS; ++s) {
+    const int c = min(s * 64 + lane, cn - 1);
+    if constexpr (KEY32) key[s] = ((const uint32_t*)P)[base + c];
+    else key[s] = ((const uint16_t*)P)[base + c];
+  }
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    uint32_t k;
+    if constexpr (KEY32) k = ls_order_key32(key[s]);
+    else k = ls_order_key16((uint16_t)key[s]);
+    key[s] = s * 64 + lane < cn ? k : 0u;
+  }
+  uint32_t T = 0;
+#pragma unroll 1
+  for (int bit = KEY32 ? 31 : 15; bit >= 0; --bit) {
+    const uint32_t cand = T | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) cnt += __popcll(__ballot(key[s] >= cand));
+    if (cnt >= kk) T = cand;
+  }
+  int gt = 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) gt += __popcll(__ballot(key[s] > T));
+  const int m = kk - gt;
+
+  int out_pos = lo_end, eq_before = 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int c = s * 64 + lane;
+    const bool valid = c < cn;
+    const bool eq = valid && key[s] == T;
+    const uint64_t eq_mask = __ballot(eq);
+    const int eq_rank = eq_before + ls_lanes_below(eq_mask);
+    const bool sel = valid && (key[s] > T || (eq && eq_rank < m));
+    const uint64_t sel_mask = __ballot(sel);
+    if (sel) orow[out_pos + ls_lanes_below(sel_mask)] = lo_end + c;
+    out_pos += __popcll(sel_mask);
+    eq_before += __popcll(eq_mask);
+  }
 }
 
 template <int KPL, bool KEY32>
@@ -278,7 +463,8 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
     const int32_t* __restrict__ cu_a, int batch, int64_t total_q, int G, int take,
     int init_blocks, int local_blocks, int block_size, int32_t* __restrict__ topk_idx) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // The wave index is uniform: keep the row and everything derived from it scalar.
+  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (row >= (int64_t)G * total_q) return;
   const int g = (int)(row / total_q);
   const int64_t t = row - (int64_t)g * total_q;
@@ -306,50 +492,22 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
   const int kk = n_valid - n_forced;
   const int cn = hi_start - lo_end;
 
-  uint32_t key[KPL];
-  const int64_t base = row * p_stride + lo_end;
-#pragma unroll
-  for (int s = 0; s < KPL; ++s) {
-    const int c = s * 64 + lane;
-    uint32_t k = 0;
-    if (c < cn) {
-      if constexpr (KEY32) k = ls_order_key32(((const uint32_t*)P)[base + c]);
-      else k = ls_order_key16(((const uint16_t*)P)[base + c]);
-    }
-    key[s] = k;
-  }
-  uint32_t T = 0;
-  for (int bit = KEY32 ? 31 : 15; bit >= 0; --bit) {
-    const uint32_t cand = T | (1u << bit);
-    int cnt = 0;
-#pragma unroll
-    for (int s = 0; s < KPL; ++s) cnt += key[s] >= cand;
-    if (ls_wave_sum(cnt) >= kk) T = cand;
-  }
-  int gt = 0;
-#pragma unroll
-  for (int s = 0; s < KPL; ++s) gt += key[s] > T;
-  const int m = kk - ls_wave_sum(gt);
-
   for (int i = lane; i < lo_end; i += 64) orow[i] = i;
   const int hi_pos = lo_end + kk;
   for (int i = lane; i < qp + 1 - hi_start; i += 64) orow[hi_pos + i] = hi_start + i;
 
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int out_pos = lo_end, eq_before = 0;
-#pragma unroll
-  for (int s = 0; s < KPL; ++s) {
-    const int c = s * 64 + lane;
-    const bool valid = c < cn;
-    const bool eq = valid && key[s] == T;
-    const uint64_t eq_mask = __ballot(eq);
-    const int eq_rank = eq_before + __popcll(eq_mask & lt_mask);
-    const bool sel = valid && (key[s] > T || (eq && eq_rank < m));
-    const uint64_t sel_mask = __ballot(sel);
-    if (sel) orow[out_pos + __popcll(sel_mask & lt_mask)] = lo_end + c;
-    out_pos += __popcll(sel_mask);
-    eq_before += __popcll(eq_mask);
-  }
+  // Candidates in registers, NS slots of 64; the row's slot count is uniform,
+  // so the branch picks one straight-line body per wave.
+  const int64_t base = row * p_stride + lo_end;
+  const int n_slots = (cn + 63) >> 6;
+  if (n_slots <= 1) return ls_topk_row<1, KEY32>(P, base, cn, kk, lo_end, lane, orow);
+  if (n_slots <= 2) return ls_topk_row<2, KEY32>(P, base, cn, kk, lo_end, lane, orow);
+  if (n_slots <= 4 || KPL <= 4) return ls_topk_row<(KPL < 4 ? KPL : 4), KEY32>(P, base, cn, kk, lo_end, lane, orow);
+  if (n_slots <= 8 || KPL <= 8) return ls_topk_row<(KPL < 8 ? KPL : 8), KEY32>(P, base, cn, kk, lo_end, lane, orow);
+  if (n_slots <= 16 || KPL <= 16) return ls_topk_row<(KPL < 16 ? KPL : 16), KEY32>(P, base, cn, kk, lo_end, lane, orow);
+  if (n_slots <= 32 || KPL <= 32) return ls_topk_row<(KPL < 32 ? KPL : 32), KEY32>(P, base, cn, kk, lo_end, lane, orow);
+  if (n_slots <= 64 || KPL <= 64) return ls_topk_row<(KPL < 64 ? KPL : 64), KEY32>(P, base, cn, kk, lo_end, lane, orow);
+  return ls_topk_row<KPL, KEY32>(P, base, cn, kk, lo_end, lane, orow);
 }
 
 // ---------------------------------------------------------------------------
@@ -417,6 +575,13 @@ int launch_proj16(const void* A, int64_t lda, int64_t gk, int64_t M, int K, int 
   const uint16_t* a = (const uint16_t*)A;
   const uint16_t* w = (const uint16_t*)wt;
   uint16_t* o = (uint16_t*)out;
+  if (K % 128 == 0 && F % 64 == 0 && F <= 128) {  // LDS-staged weight tiles
+    if (F == 64)
+      hipLaunchKernelGGL((ls_proj_tile_kernel<DT, 4>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o);
+    else
+      hipLaunchKernelGGL((ls_proj_tile_kernel<DT, 8>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o);
+    return ls_check_launch("ls_proj_tile_kernel");
+  }
   switch (F / 16) {
     case 2: hipLaunchKernelGGL((ls_proj_mfma_kernel<DT, 2>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o); break;
     case 4: hipLaunchKernelGGL((ls_proj_mfma_kernel<DT, 4>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o); break;
