@@ -75,6 +75,30 @@ def test_select_32k_sampled_rows():
     assert rep.exact_rows >= 0.97 * rep.rows
 
 
+def test_select_128k_sampled_rows():
+    """Every per-row slot count of the 128K layer (1..32 slots of 64 candidates)."""
+    case = workloads.hidden_space_layer((131072,), device=DEV, seed=5)
+    rows = spread_rows(case.cu_host, per_seq=96)
+    _, _, ids, rep = _check_select(case, rows=rows)
+    assert rep.exact_rows >= 0.97 * rep.rows
+
+
+def test_select_300k_ragged_widest_slots():
+    """Candidate rows longer than 4096 pages (128 register slots) next to a short sequence."""
+    case = workloads.hidden_space_layer((300000, 5000), device=DEV, seed=6)
+    rows = spread_rows(case.cu_host, per_seq=48)
+    _, _, ids, rep = _check_select(case, rows=rows)
+    assert rep.exact_rows >= 0.97 * rep.rows
+
+
+def test_select_fp32_160k_sampled_rows():
+    """float32 scores (32-bit keys) with 64 register slots; float32 rows are bit-exact."""
+    case = workloads.head_space_layer(160000, device=DEV, seed=7)
+    rows = spread_rows(case.cu_host, per_seq=64)
+    _, _, ids, rep = _check_select(case, rows=rows)
+    assert rep.exact_rows == rep.rows
+
+
 def _attention_case(dtype=torch.bfloat16, lens=(3000,), seed=4, **kw):
     case = workloads.hidden_space_layer(lens, device=DEV, dtype=dtype, seed=seed, **kw)
     _, _, ids = _select(case)
