@@ -199,7 +199,7 @@ def main() -> None:
         "stages_ms": {"compress_k": round(ms_compress, 4), "select": round(ms_select, 4),
                       "sparse_attention": round(ms_attn, 4)},
         "roofline": {
-            "kernel": "ls_attn_kernel (block-sparse attention op incl. V staging)",
+            "kernel": "ls_attn_tile_kernel (block-sparse attention; V staging and plan kernels excluded)",
             "bound": "mfma",
             "achieved": round(attn_tflops, 2),
             "peak": BF16_PEAK_TFLOPS,

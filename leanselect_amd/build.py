@@ -30,6 +30,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-file additions.  The attention kernel only handles finite and -inf
+# scores, so it is built without IEEE NaN quieting: maxima then need no
+# canonicalising moves and fuse into v_max3.
+FILE_FLAGS = {
+    "ls_attention": ["-mno-amdgpu-ieee", "-fno-honor-nans"],
+}
+
+
 def _hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(exe).exists():
@@ -39,7 +47,8 @@ def _hipcc() -> str:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-I", str(PKG.parent / "include"), "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.stem, []), "-I", str(PKG.parent / "include"),
+           "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

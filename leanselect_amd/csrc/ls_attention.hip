@@ -22,6 +22,14 @@
 //     exact per-page power-of-two scale that moves onto P), output rounded once.
 #include "ls_common.h"
 
+// Work-item and workgroup ids straight from the hardware: this file is built
+// without IEEE NaN quieting, and the device library's id helpers (built with
+// it) would then stay out-of-line calls.
+#define LS_TID ((int)__builtin_amdgcn_workitem_id_x())
+#define LS_BID_X ((int)__builtin_amdgcn_workgroup_id_x())
+#define LS_BID_Y ((int)__builtin_amdgcn_workgroup_id_y())
+#define LS_BID_Z ((int)__builtin_amdgcn_workgroup_id_z())
+
 #define LS_ATTN_MAX_PAGES 8192
 #define LS_ATTN_MAX_TAKE 128
 
@@ -48,7 +56,7 @@ __device__ __forceinline__ int ls_wave_excl_scan(int v, int lane, int* total) {
 __global__ void ls_attn_plan_kernel(const int32_t* __restrict__ cu_q,
                                     const int32_t* __restrict__ cu_k, int batch, int tile,
                                     int32_t* __restrict__ pg_off, int32_t* __restrict__ tile_off) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  if (LS_TID != 0 || LS_BID_X != 0) return;
   int32_t acc = 0, acc_t = 0;
   pg_off[0] = 0;
   tile_off[0] = 0;
@@ -77,16 +85,16 @@ __global__ __launch_bounds__(256) void ls_vt_kernel(const uint16_t* __restrict__
   constexpr int PITCH = D + 2;
   __shared__ uint16_t tile[64 * PITCH];
   __shared__ float wave_max[4];
-  const int64_t tile_id = blockIdx.x;
+  const int64_t tile_id = LS_BID_X;
   if (tile_id >= pg_off[batch]) return;
-  const int g = blockIdx.y;
+  const int g = LS_BID_Y;
   const int b = ls_find_segment(pg_off, batch, tile_id);
   const int p = (int)(tile_id - pg_off[b]);
   const int lk = cu_k[b + 1] - cu_k[b];
   const int64_t krow0 = (int64_t)cu_k[b] + 64LL * p;
   constexpr int CH = D / 8;  // 16-byte chunks per row
   float mx = 0.f;
-  for (int c = threadIdx.x; c < 64 * CH; c += 256) {
+  for (int c = LS_TID; c < 64 * CH; c += 256) {
     const int key = c / CH, d0 = (c % CH) * 8;
     ls_u32x4 val = {0u, 0u, 0u, 0u};
     if (64 * p + key < lk) val = ls_load16(v + (krow0 + key) * v_rs + (int64_t)g * D + d0);
@@ -100,15 +108,15 @@ __global__ __launch_bounds__(256) void ls_vt_kernel(const uint16_t* __restrict__
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, LS_WAVE));
-  if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = mx;
+  if ((LS_TID & 63) == 0) wave_max[LS_TID >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
   int e = 0;
   while (e < 15 && mx * __builtin_ldexpf(1.f, -e) > 32768.f) ++e;
   const float scale = __builtin_ldexpf(1.f, -e);
-  if (threadIdx.x == 0) vexp[(int64_t)g * n_pages + pg_off[b] + p] = e;
+  if (LS_TID == 0) vexp[(int64_t)g * n_pages + pg_off[b] + p] = e;
   const int64_t col0 = 64LL * (pg_off[b] + p);
-  for (int c = threadIdx.x; c < D * 8; c += 256) {
+  for (int c = LS_TID; c < D * 8; c += 256) {
     const int d = c / 8, k0 = (c % 8) * 8;
     ls_u32x4 o;
 #pragma unroll
@@ -120,16 +128,22 @@ __global__ __launch_bounds__(256) void ls_vt_kernel(const uint16_t* __restrict__
 }
 
 // ---------------------------------------------------------------------------
-// Tile kernel: one workgroup = 16 consecutive query rows of one sequence and
-// one KV group (8 waves x 2 rows).  The rows' page plans are OR-ed into a
-// sorted union page list; each union page of K and V^T is streamed once into
-// a 4-stage LDS ring with direct global->LDS loads issued three pages ahead,
-// and every row that selected the page runs its MFMAs on it.  Rows that did
-// not select a page skip it (no masked-out work).
+// Tile kernel: one workgroup = 32 consecutive query rows of one sequence and
+// one KV group (4 waves x 8 rows, one wave per SIMD).  The rows' page plans
+// are OR-ed into a sorted union page list; each union page of K and V^T is
+// streamed once into a 4-stage LDS ring with direct global->LDS loads issued
+// three pages ahead, and every row that selected the page runs its MFMAs on
+// it.  Rows that did not select a page skip it (no masked-out work).  A wave
+// keeps its eight rows' O^T accumulators (8 x 32 floats per lane) in the
+// accumulation registers and their Q^T fragments in vector registers.
 // ---------------------------------------------------------------------------
-#define LS_ATT_WAVES 8                       // waves per workgroup
+#ifndef LS_ATT_TPW
 #define LS_ATT_TPW 2                         // rows per wave
-#define LS_ATT_TILE (LS_ATT_WAVES * LS_ATT_TPW)  // rows per workgroup
+#endif
+#ifndef LS_ATT_WAVES
+#define LS_ATT_WAVES 8                       // waves per workgroup
+#endif
+#define LS_ATT_TILE (LS_ATT_WAVES * LS_ATT_TPW)  // rows per workgroup (<= 32)
 #define LS_ATT_THREADS (64 * LS_ATT_WAVES)
 // 16-byte global->LDS copies per page issued by each wave: K is 64 rows of
 // 256 B (4 rows per copy), V^T 128 rows of 128 B (8 rows per copy).
@@ -140,8 +154,11 @@ __global__ __launch_bounds__(256) void ls_vt_kernel(const uint16_t* __restrict__
 #define LS_ATT_KBYTES (64 * 256)             // K page: 64 rows x 256 B
 #define LS_ATT_STAGE_BYTES (2 * LS_ATT_KBYTES)  // + V^T page: 128 rows x 128 B
 #define LS_ATT_WORDS (LS_ATTN_MAX_PAGES / 32)
+#define LS_ATT_MAX_UNION (LS_ATT_TILE * LS_ATTN_MAX_TAKE)
 
 typedef __attribute__((address_space(3))) void ls_lds_void;
+typedef _Float16 ls_half2 __attribute__((ext_vector_type(2)));
+typedef float ls_float2 __attribute__((ext_vector_type(2)));
 
 // LDS row of key j (0..63) of a page: inside each 32-key chunk, MFMA row r of
 // key block nb holds key 8*(r/4) + 4*nb + r%4, so storing that key at row
@@ -152,24 +169,36 @@ __device__ __forceinline__ int ls_att_key_of_row(int row) {
   return 32 * c + 8 * (r >> 2) + 4 * nb + (r & 3);
 }
 
-// One 16-byte global->LDS load per lane (lane l lands at lds_off + 16 l; the
-// offset is wave-uniform).  Issued as inline asm so the compiler's wait
-// insertion does not treat every later LDS read as aliasing the in-flight
-// copy (which would drain the whole prefetch queue); the kernel orders the
-// copies itself with vmcnt waits and a barrier per page.
-__device__ __forceinline__ void ls_dma16(const void* gsrc, uint32_t lds_off) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+// One 16-byte global->LDS load per lane from sbase + voff bytes (lane l lands
+// at lds_off + 16 l; sbase and lds_off are wave-uniform, voff a 32-bit lane
+// offset).  Issued as inline asm so the compiler's wait insertion does not
+// treat every later LDS read as aliasing the in-flight copy (which would
+// drain the whole prefetch queue); the kernel orders the copies itself with
+// vmcnt waits and a barrier per page.  An SALU write of M0 followed by a
+// global load with LDS destination needs one wait state, which the compiler
+// cannot insert inside the asm block.
+__device__ __forceinline__ void ls_dma16(const void* sbase, uint32_t voff, uint32_t lds_off) {
+  const uint64_t a = (uint64_t)(uintptr_t)sbase;
+  // (readfirstlane returns int: widen each half as unsigned, or the low half
+  // would be sign-extended into the high one.)
+  const uint64_t sa = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
+                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(gsrc), "s"(lds_off)
+               : "v"(voff), "s"(sa), "s"(lds_off)
                : "memory", "m0");
 }
 
-// max of three floats in one instruction (inputs are finite or -inf scores, so
-// the NaN quieting that fmaxf would add is not needed).
-__device__ __forceinline__ float ls_max3(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
+// Two float32 -> one packed fp16 pair (round to nearest even).
+__device__ __forceinline__ uint32_t ls_pack_f16x2(float a, float b) {
+  const ls_half2 h = __builtin_convertvector((ls_float2){a, b}, ls_half2);
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// acc + lo(x) + hi(x) for a packed fp16 pair, in float32.
+__device__ __forceinline__ float ls_sum_f16x2(uint32_t x, float acc) {
+  const ls_half2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(ls_half2, x), one, acc, false);
 }
 
 // vmcnt(n) with the other counters left alone (gfx9 encoding).
@@ -177,33 +206,44 @@ __device__ __forceinline__ float ls_max3(float a, float b, float c) {
   __builtin_amdgcn_s_waitcnt(((n) & 0xf) | (((n) >> 4) << 14) | (0x7 << 4) | (0xf << 8))
 
 template <int DT>
-__global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
+__global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_tile_kernel(
     const uint16_t* __restrict__ qg, int64_t q_rs, const uint16_t* __restrict__ kg,
     int64_t k_rs, const uint16_t* __restrict__ vt, int64_t lpad,
     const int32_t* __restrict__ vexp, int64_t n_pages_ws,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
     const int32_t* __restrict__ pg_off, const int32_t* __restrict__ tile_off, int batch,
     int64_t total_q, int G, int gs, const int32_t* __restrict__ topk_idx, int take,
-    float scale_log2, int causal, uint16_t* __restrict__ out, float* __restrict__ lse) {
+    float scale_log2, int causal, uint16_t* __restrict__ out, float* __restrict__ lse,
+    int per_xcd) {
   constexpr int D = 128;
+  constexpr uint32_t ROWS_MASK = LS_ATT_TPW == 32 ? 0xffffffffu : ((1u << LS_ATT_TPW) - 1u);
+  // The per-row page bitmaps are only needed before streaming starts and
+  // share their LDS with the ring.
   __shared__ __align__(16) uint8_t s_ring[LS_ATT_STAGES * LS_ATT_STAGE_BYTES];
-  __shared__ uint32_t s_bits[LS_ATT_TILE][LS_ATT_WORDS];
-  __shared__ uint16_t s_union[LS_ATT_TILE * LS_ATTN_MAX_TAKE];
-  __shared__ int8_t s_uexp[LS_ATT_TILE * LS_ATTN_MAX_TAKE];
-  __shared__ uint16_t s_umask[LS_ATT_TILE * LS_ATTN_MAX_TAKE];
+  __shared__ uint16_t s_union[LS_ATT_MAX_UNION];
+  __shared__ int8_t s_uexp[LS_ATT_MAX_UNION];
+  __shared__ uint32_t s_umask[LS_ATT_MAX_UNION];
   __shared__ int s_wsum[LS_ATT_WAVES];
+  static_assert(LS_ATT_TILE * LS_ATT_WORDS * 4 <= LS_ATT_STAGES * LS_ATT_STAGE_BYTES,
+                "page bitmaps must fit in the ring");
+  static_assert(LS_ATT_TILE <= 32, "row masks are 32-bit");
+  static_assert(LS_ATT_WORDS <= LS_ATT_THREADS, "one bitmap word per thread");
+#ifdef LS_ATT_NO_ALIAS
+  __shared__ uint32_t s_bits[LS_ATT_TILE][LS_ATT_WORDS];
+#else
+  uint32_t(*s_bits)[LS_ATT_WORDS] = reinterpret_cast<uint32_t(*)[LS_ATT_WORDS]>(s_ring);
+#endif
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int tid = LS_TID;
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, q = lane >> 4;
 
   // XCD-aware tile order: consecutive workgroups land on different XCDs, so
   // give each XCD a contiguous run of tiles (neighbouring rows share pages).
-  const int per_xcd = gridDim.x / 8;
-  const int64_t tile = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  const int64_t tile = (int64_t)(LS_BID_X % 8) * per_xcd + LS_BID_X / 8;
   if (tile >= tile_off[batch]) return;
-  const int g = blockIdx.y;
-  const int head = blockIdx.z * 16 + r;
+  const int g = LS_BID_Y;
+  const int head = LS_BID_Z * 16 + r;
   const bool head_ok = head < gs;
 
   const int b = ls_find_segment(tile_off, batch, tile);
@@ -263,7 +303,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
 #pragma unroll
     for (int i = 0; i < LS_ATT_TILE; ++i) rows |= ((s_bits[i][tid] >> bit) & 1u) << i;
     s_uexp[pos] = (int8_t)vexp_seq[page];
-    s_umask[pos] = (uint16_t)rows;
+    s_umask[pos] = rows;
     s_union[pos++] = (uint16_t)page;
   }
 
@@ -291,7 +331,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[j][db] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  __syncthreads();  // union list, exponents and every wave's Q loads are complete
+  __syncthreads();  // union list, exponents and every wave's Q loads are complete;
+                    // the bitmaps are dead, so the ring may be written
   LS_WAIT_VMCNT(0);
 
   // ---- staging: wave w moves K rows 4*K_COPIES*w.. and V^T rows 8*V_COPIES*w.. ----
@@ -303,24 +344,30 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
   const uint16_t* vgrp = vt + (int64_t)g * D * lpad + vbase;
   const uint32_t ring_off = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(ls_lds_void*)s_ring);
+  const int64_t k_rs_bytes = 2 * k_rs;
   auto issue = [&](int page, int stage) {
+    page = __builtin_amdgcn_readfirstlane(page);
     const uint32_t kb = ring_off + stage * LS_ATT_STAGE_BYTES;
     const uint32_t vb = kb + LS_ATT_KBYTES;
+    // Keys past the sequence end repeat its last key (their scores are masked).
+    const int key_rem = lk - 1 - 64 * page;  // >= 0: every union page is visible
+    const int key_lim = key_rem < 63 ? key_rem : 63;
+    const uint16_t* kpage = kgrp + (kstart + 64LL * page) * k_rs;
 #pragma unroll
     for (int i = 0; i < LS_ATT_K_COPIES; ++i) {
       const int R0 = 4 * (LS_ATT_K_COPIES * w + i);
       const int R = R0 + (lane >> 4);
       const int C = (lane & 15) ^ (R & 15);
-      const int64_t kr = min((int64_t)64 * page + ls_att_key_of_row(R), (int64_t)lk - 1);
-      ls_dma16(kgrp + (kstart + kr) * k_rs + 8 * C, __builtin_amdgcn_readfirstlane(kb + R0 * 256));
+      const uint32_t voff = (uint32_t)(min(ls_att_key_of_row(R), key_lim) * k_rs_bytes) + 16u * C;
+      ls_dma16(kpage, voff, __builtin_amdgcn_readfirstlane(kb + R0 * 256));
     }
+    const uint16_t* vpage = vgrp + 64LL * page;
 #pragma unroll
     for (int i = 0; i < LS_ATT_V_COPIES; ++i) {
       const int d0 = 8 * (LS_ATT_V_COPIES * w + i);
       const int d = d0 + (lane >> 3);
       const int C = (lane & 7) ^ ((d >> 1) & 7);
-      ls_dma16(vgrp + (int64_t)d * lpad + 64LL * page + 8 * C,
-               __builtin_amdgcn_readfirstlane(vb + d0 * 128));
+      ls_dma16(vpage, (uint32_t)(d * 2 * lpad) + 16u * C, __builtin_amdgcn_readfirstlane(vb + d0 * 128));
     }
   };
 
@@ -339,8 +386,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
       issue(s_union[ui + LS_ATT_STAGES - 1], (ui + LS_ATT_STAGES - 1) % LS_ATT_STAGES);
 
     const int page = s_union[ui];
-    const int sel = __builtin_amdgcn_readfirstlane(
-        (s_umask[ui] >> (LS_ATT_TPW * w)) & ((1 << LS_ATT_TPW) - 1));
+    const uint32_t sel = __builtin_amdgcn_readfirstlane((s_umask[ui] >> (LS_ATT_TPW * w)) & ROWS_MASK);
     if (!sel) continue;
     const int v_e = s_uexp[ui];
     const float p_unscale = __builtin_ldexpf(1.f, -v_e);
@@ -349,9 +395,9 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const int base = 64 * page + 32 * c;
-      int need = 0;
+      uint32_t need = 0;
 #pragma unroll
-      for (int j = 0; j < LS_ATT_TPW; ++j) need |= (((sel >> j) & 1) && base <= jmax_r[j]) << j;
+      for (int j = 0; j < LS_ATT_TPW; ++j) need |= (uint32_t)(((sel >> j) & 1u) && base <= jmax_r[j]) << j;
       need = __builtin_amdgcn_readfirstlane(need);
       if (!need) continue;
       // The chunk's K and V^T fragments are read once and shared by the rows.
@@ -368,24 +414,29 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
 #pragma unroll
       for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
       const int key0 = base + 8 * q;
-#pragma unroll
-      for (int j = 0; j < LS_ATT_TPW; ++j) {
-        if (!((need >> j) & 1)) continue;
-        ls_f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      // S^T of one row: lane (r, q) gets head r's raw scores of keys base + 8q + 0..7.
+      auto qk = [&](int j, ls_f32x4& s0, ls_f32x4& s1) {
+        s0 = ls_f32x4{0.f, 0.f, 0.f, 0.f};
+        s1 = ls_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           s0 = LsElem<DT>::mfma(kf0[ks], qf[j][ks], s0);
           s1 = LsElem<DT>::mfma(kf1[ks], qf[j][ks], s1);
         }
-        // Lane (r, q) holds head r's raw scores of keys base + 8q + 0..7.
+      };
+      // Online softmax update of row j with its chunk scores, then O^T += V^T P^T.
+      auto soft_pv = [&](int j, const ls_f32x4& s0, const ls_f32x4& s1) {
         float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
         if (base + 31 > jmax_r[j]) {  // the chunk crosses this row's causal frontier
 #pragma unroll
           for (int i = 0; i < 8; ++i)
             if (key0 + i > jmax_r[j]) sv[i] = -INFINITY;
         }
-        const float lmax = fmaxf(ls_max3(sv[0], sv[1], sv[2]),
-                                 ls_max3(ls_max3(sv[3], sv[4], sv[5]), sv[6], sv[7]));
+        // Plain maxima: the compiler inserts the wait states an MFMA result
+        // needs before a VALU read (it cannot for inline asm), and this file is
+        // built without IEEE NaN quieting, so they fuse into v_max3.
+        const float lmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), sv[2]),
+                                 fmaxf(fmaxf(fmaxf(sv[3], sv[4]), sv[5]), fmaxf(sv[6], sv[7])));
         // Rescale only when some head's max grows by more than 2^8 (or when the
         // page's V scale leaves too little fp16 headroom for P up to 2^8).
         if (__ballot(lmax > thr[j]) != 0ull || v_e > 7) {
@@ -400,20 +451,25 @@ __global__ __launch_bounds__(LS_ATT_THREADS, 2) void ls_attn_tile_kernel(
 #pragma unroll
           for (int db = 0; db < 8; ++db) o[j][db] *= alpha;
         }
-        // P' = P * 2^e (the page's V scale moved onto P, exact): one exp each.
+        // P' = P * 2^e (the page's V scale moved onto P, exact): one exp each;
+        // the row sum adds the fp16 P' that the MFMA uses, scaled back by 2^-e.
         const float bias = (float)v_e - m_run[j];
-        float pv[8], lsum = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          pv[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], scale_log2, bias));
-          lsum += pv[i];
-        }
-        l_run[j] += v_e ? lsum * p_unscale : lsum;
         ls_u32x4 pf;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pf[i] = ls_pack2(ls_f32_to_f16(pv[2 * i]), ls_f32_to_f16(pv[2 * i + 1]));
+        for (int i = 0; i < 4; ++i)
+          pf[i] = ls_pack_f16x2(__builtin_amdgcn_exp2f(fmaf(sv[2 * i], scale_log2, bias)),
+                                __builtin_amdgcn_exp2f(fmaf(sv[2 * i + 1], scale_log2, bias)));
+        const float lsum = ls_sum_f16x2(pf[3], ls_sum_f16x2(pf[2], ls_sum_f16x2(pf[1], ls_sum_f16x2(pf[0], 0.f))));
+        l_run[j] = fmaf(lsum, p_unscale, l_run[j]);
 #pragma unroll
         for (int db = 0; db < 8; ++db) o[j][db] = LsElem<LS_F16>::mfma(vf[db], pf, o[j][db]);
+      };
+#pragma unroll
+      for (int j = 0; j < LS_ATT_TPW; ++j) {
+        if (!((need >> j) & 1u)) continue;
+        ls_f32x4 s0, s1;
+        qk(j, s0, s1);
+        soft_pv(j, s0, s1);
       }
     }
   }
@@ -502,6 +558,8 @@ extern "C" int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const 
              LS_ERR_UNSUPPORTED,
              "ls_sparse_attn_varlen: tensors must be 16-byte aligned with row strides %% 8 == 0");
   const AttnWs L = attn_ws(total_k, batch, num_kv_heads, head_dim, 2);
+  LS_REQUIRE(L.lpad * 2 * head_dim < (1LL << 32) && 64LL * k_row_stride * 2 < (1LL << 31),
+             LS_ERR_UNSUPPORTED, "ls_sparse_attn_varlen: too many keys for 32-bit copy offsets");
   LS_REQUIRE(workspace && workspace_bytes >= L.total, LS_ERR_WORKSPACE,
              "ls_sparse_attn_varlen: workspace needs %zu bytes", L.total);
   hipStream_t s = (hipStream_t)stream;
@@ -533,11 +591,13 @@ extern "C" int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const 
     hipLaunchKernelGGL(ls_attn_tile_kernel<LS_BF16>, grid, dim3(LS_ATT_THREADS), 0, s, (const uint16_t*)q,
                        q_row_stride, (const uint16_t*)k, k_row_stride, vt, L.lpad, vexp,
                        L.n_pages, cu_seqlens_q, cu_seqlens_k, pg, tiles, batch, total_q,
-                       num_kv_heads, gs, topk_idx, take, scale_log2, causal, (uint16_t*)out, lse);
+                       num_kv_heads, gs, topk_idx, take, scale_log2, causal, (uint16_t*)out, lse,
+                       (int)(grid.x / 8));
   else
     hipLaunchKernelGGL(ls_attn_tile_kernel<LS_F16>, grid, dim3(LS_ATT_THREADS), 0, s, (const uint16_t*)q,
                        q_row_stride, (const uint16_t*)k, k_row_stride, vt, L.lpad, vexp,
                        L.n_pages, cu_seqlens_q, cu_seqlens_k, pg, tiles, batch, total_q,
-                       num_kv_heads, gs, topk_idx, take, scale_log2, causal, (uint16_t*)out, lse);
+                       num_kv_heads, gs, topk_idx, take, scale_log2, causal, (uint16_t*)out, lse,
+                       (int)(grid.x / 8));
   return ls_check_launch("ls_attn_tile_kernel");
 }
