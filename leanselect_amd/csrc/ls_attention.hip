@@ -145,11 +145,6 @@ __global__ __launch_bounds__(256) void ls_vt_kernel(const uint16_t* __restrict__
 #endif
 #define LS_ATT_TILE (LS_ATT_WAVES * LS_ATT_TPW)  // rows per workgroup (<= 32)
 #define LS_ATT_THREADS (64 * LS_ATT_WAVES)
-// 16-byte global->LDS copies per page issued by each wave: K is 64 rows of
-// 256 B (4 rows per copy), V^T 128 rows of 128 B (8 rows per copy).
-#define LS_ATT_K_COPIES (64 / LS_ATT_WAVES / 4)
-#define LS_ATT_V_COPIES (128 / LS_ATT_WAVES / 8)
-#define LS_ATT_COPIES (LS_ATT_K_COPIES + LS_ATT_V_COPIES)
 #define LS_ATT_STAGES 4
 #define LS_ATT_KBYTES (64 * 256)             // K page: 64 rows x 256 B
 #define LS_ATT_STAGE_BYTES (2 * LS_ATT_KBYTES)  // + V^T page: 128 rows x 128 B
@@ -224,6 +219,10 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   __shared__ int8_t s_uexp[LS_ATT_MAX_UNION];
   __shared__ uint32_t s_umask[LS_ATT_MAX_UNION];
   __shared__ int s_wsum[LS_ATT_WAVES];
+  // Ring protocol: s_next = next union page to be claimed for copying;
+  // s_ready[st] = union index + 1 of the page whose copy into stage st has
+  // landed; s_done[st] = waves finished with stage st, over all its pages.
+  __shared__ uint32_t s_next, s_ready[LS_ATT_STAGES], s_done[LS_ATT_STAGES];
   static_assert(LS_ATT_TILE * LS_ATT_WORDS * 4 <= LS_ATT_STAGES * LS_ATT_STAGE_BYTES,
                 "page bitmaps must fit in the ring");
   static_assert(LS_ATT_TILE <= 32, "row masks are 32-bit");
@@ -267,6 +266,11 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
 
   // ---- per-row page bitmaps and their sorted union ----
   for (int i = tid; i < LS_ATT_TILE * nwords; i += LS_ATT_THREADS) s_bits[i / nwords][i % nwords] = 0u;
+  if (tid < LS_ATT_STAGES) {
+    s_ready[tid] = 0u;
+    s_done[tid] = 0u;
+  }
+  if (tid == 0) s_next = 0u;
   __syncthreads();
   if (last_page >= 0) {
     const int32_t* ids = topk_idx + ((int64_t)g * total_q + t0) * take;
@@ -335,59 +339,87 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
                     // the bitmaps are dead, so the ring may be written
   LS_WAIT_VMCNT(0);
 
-  // ---- staging: wave w moves K rows 4*K_COPIES*w.. and V^T rows 8*V_COPIES*w.. ----
-  // K row R holds key ls_att_key_of_row(R) with its 16-byte chunk C stored at
-  // position C ^ (R & 15); V^T row d (8 chunks) at position C ^ ((d >> 1) & 7).
-  // The sixteen lanes of an MFMA operand read then hit sixteen distinct bank
+  // ---- staging ----
+  // One wave copies a whole union page into its stage: K as 64 rows of 256 B
+  // (row R holds key ls_att_key_of_row(R), 16-byte chunk C at position
+  // C ^ (R & 15)) and V^T as 128 rows of 128 B (chunk C at C ^ ((d >> 1) & 7)),
+  // so the sixteen lanes of an MFMA operand read hit sixteen distinct bank
   // groups.  Each copy fills 1 KB of contiguous LDS (lane l -> byte 16 l).
+  //
+  // Waves are not kept in lockstep.  Before each page a wave claims the next
+  // unclaimed page (at most three ahead of itself) once every wave is done
+  // with that page's stage, copies it, and marks it ready one page later.  A
+  // wave waits only for the page it is about to read, and marks its own
+  // claimed copy ready before it waits, so every waiting wave depends only on
+  // copies that are already marked or still being issued.
   const uint16_t* kgrp = kg + (int64_t)g * D;
   const uint16_t* vgrp = vt + (int64_t)g * D * lpad + vbase;
   const uint32_t ring_off = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(ls_lds_void*)s_ring);
   const int64_t k_rs_bytes = 2 * k_rs;
-  auto issue = [&](int page, int stage) {
-    page = __builtin_amdgcn_readfirstlane(page);
-    const uint32_t kb = ring_off + stage * LS_ATT_STAGE_BYTES;
+  auto issue_page = [&](int ui_copy) {
+    const int page = __builtin_amdgcn_readfirstlane((int)s_union[ui_copy]);
+    const uint32_t kb = ring_off + (ui_copy % LS_ATT_STAGES) * LS_ATT_STAGE_BYTES;
     const uint32_t vb = kb + LS_ATT_KBYTES;
     // Keys past the sequence end repeat its last key (their scores are masked).
     const int key_rem = lk - 1 - 64 * page;  // >= 0: every union page is visible
     const int key_lim = key_rem < 63 ? key_rem : 63;
     const uint16_t* kpage = kgrp + (kstart + 64LL * page) * k_rs;
 #pragma unroll
-    for (int i = 0; i < LS_ATT_K_COPIES; ++i) {
-      const int R0 = 4 * (LS_ATT_K_COPIES * w + i);
-      const int R = R0 + (lane >> 4);
+    for (int i = 0; i < 16; ++i) {
+      const int R = 4 * i + (lane >> 4);
       const int C = (lane & 15) ^ (R & 15);
       const uint32_t voff = (uint32_t)(min(ls_att_key_of_row(R), key_lim) * k_rs_bytes) + 16u * C;
-      ls_dma16(kpage, voff, __builtin_amdgcn_readfirstlane(kb + R0 * 256));
+      ls_dma16(kpage, voff, kb + i * 1024);
     }
     const uint16_t* vpage = vgrp + 64LL * page;
 #pragma unroll
-    for (int i = 0; i < LS_ATT_V_COPIES; ++i) {
-      const int d0 = 8 * (LS_ATT_V_COPIES * w + i);
-      const int d = d0 + (lane >> 3);
+    for (int i = 0; i < 16; ++i) {
+      const int d = 8 * i + (lane >> 3);
       const int C = (lane & 7) ^ ((d >> 1) & 7);
-      ls_dma16(vpage, (uint32_t)(d * 2 * lpad) + 16u * C, __builtin_amdgcn_readfirstlane(vb + d0 * 128));
+      ls_dma16(vpage, (uint32_t)(d * 2 * lpad) + 16u * C, vb + i * 1024);
     }
   };
+  int pending = -1;       // union index this wave copied and has not marked ready
+  int pending_since = 0;  // page at which it was claimed
+  auto try_claim = [&](int ui) {
+    if (pending >= 0) return;
+    const int nx = __builtin_amdgcn_readfirstlane(
+        (int)__hip_atomic_load(&s_next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    if (nx >= n_union || nx > ui + LS_ATT_STAGES - 1) return;
+    const uint32_t gen = (uint32_t)nx / LS_ATT_STAGES;
+    if (gen > 0 && (uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
+                       &s_done[nx % LS_ATT_STAGES], __ATOMIC_ACQUIRE,
+                       __HIP_MEMORY_SCOPE_WORKGROUP)) < LS_ATT_WAVES * gen)
+      return;  // a wave may still read the stage's previous page
+    int won = 0;
+    if (lane == 0) {
+      uint32_t expect = (uint32_t)nx;
+      won = __hip_atomic_compare_exchange_strong(&s_next, &expect, (uint32_t)nx + 1u,
+                                                 __ATOMIC_ACQ_REL, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    if (__builtin_amdgcn_readfirstlane(won)) {
+      issue_page(nx);
+      pending = nx;
+      pending_since = ui;
+    }
+  };
+  auto mark_ready = [&]() {
+    if (pending < 0) return;
+    LS_WAIT_VMCNT(0);  // this wave's copies are its only outstanding loads
+    if (lane == 0)
+      __hip_atomic_store(&s_ready[pending % LS_ATT_STAGES], (uint32_t)pending + 1u,
+                         __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    pending = -1;
+  };
+  auto is_ready = [&](int ui) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
+               &s_ready[ui % LS_ATT_STAGES], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) ==
+           (uint32_t)ui + 1u;
+  };
 
-#pragma unroll
-  for (int sidx = 0; sidx < LS_ATT_STAGES - 1; ++sidx)
-    if (sidx < n_union) issue(s_union[sidx], sidx);
-
-  for (int ui = 0; ui < n_union; ++ui) {
-    // Pages issued after page ui by this wave: min(STAGES - 2, n_union - 1 - ui).
-    const int pending = min(LS_ATT_STAGES - 2, n_union - 1 - ui);
-    if (pending >= 2) LS_WAIT_VMCNT(2 * LS_ATT_COPIES);
-    else if (pending == 1) LS_WAIT_VMCNT(LS_ATT_COPIES);
-    else LS_WAIT_VMCNT(0);
-    __syncthreads();  // page ui is in LDS for everyone; stage (ui - 1) % STAGES is free
-    if (ui + LS_ATT_STAGES - 1 < n_union)
-      issue(s_union[ui + LS_ATT_STAGES - 1], (ui + LS_ATT_STAGES - 1) % LS_ATT_STAGES);
-
-    const int page = s_union[ui];
-    const uint32_t sel = __builtin_amdgcn_readfirstlane((s_umask[ui] >> (LS_ATT_TPW * w)) & ROWS_MASK);
-    if (!sel) continue;
+  auto compute_page = [&](int ui, int page, uint32_t sel) {
     const int v_e = s_uexp[ui];
     const float p_unscale = __builtin_ldexpf(1.f, -v_e);
     const uint8_t* kb = s_ring + (ui % LS_ATT_STAGES) * LS_ATT_STAGE_BYTES;
@@ -472,7 +504,32 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
         soft_pv(j, s0, s1);
       }
     }
+  };
+
+  for (int ui = 0; ui < n_union; ++ui) {
+    try_claim(ui);
+    if (pending >= 0 && pending_since < ui) mark_ready();
+    if (!is_ready(ui)) {
+      // Bounded wait (the protocol cannot deadlock; the bound only guarantees
+      // that a wave always finishes).
+      for (int spin = 0; spin < (1 << 22); ++spin) {
+        mark_ready();
+        try_claim(ui);
+        mark_ready();
+        if (is_ready(ui)) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+
+    const int page = s_union[ui];
+    const uint32_t sel = __builtin_amdgcn_readfirstlane((s_umask[ui] >> (LS_ATT_TPW * w)) & ROWS_MASK);
+    if (sel) compute_page(ui, page, sel);
+    // Done with the stage (the release orders this wave's reads of it first).
+    if (lane == 0)
+      __hip_atomic_fetch_add(&s_done[ui % LS_ATT_STAGES], 1u, __ATOMIC_RELEASE,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
   }
+  mark_ready();
 
   // ---- epilogue ----
 #pragma unroll
