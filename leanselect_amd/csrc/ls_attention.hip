@@ -346,12 +346,12 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   // so the sixteen lanes of an MFMA operand read hit sixteen distinct bank
   // groups.  Each copy fills 1 KB of contiguous LDS (lane l -> byte 16 l).
   //
-  // Waves are not kept in lockstep.  Before each page a wave claims the next
+  // Waves are not kept in lockstep.  A wave waits only for the page it is
+  // about to read; while it waits it does the copying: it claims the next
   // unclaimed page (at most three ahead of itself) once every wave is done
-  // with that page's stage, copies it, and marks it ready one page later.  A
-  // wave waits only for the page it is about to read, and marks its own
-  // claimed copy ready before it waits, so every waiting wave depends only on
-  // copies that are already marked or still being issued.
+  // with that page's stage, copies it, waits for its own copy and marks the
+  // page ready.  Busy waves never hold an unmarked copy, so a waiting wave
+  // depends only on pages that are marked or being copied by a waiting wave.
   const uint16_t* kgrp = kg + (int64_t)g * D;
   const uint16_t* vgrp = vt + (int64_t)g * D * lpad + vbase;
   const uint32_t ring_off = __builtin_amdgcn_readfirstlane(
@@ -380,8 +380,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       ls_dma16(vpage, (uint32_t)(d * 2 * lpad) + 16u * C, vb + i * 1024);
     }
   };
-  int pending = -1;       // union index this wave copied and has not marked ready
-  int pending_since = 0;  // page at which it was claimed
+  int pending = -1;  // union index this wave copied and has not marked ready
   auto try_claim = [&](int ui) {
     if (pending >= 0) return;
     const int nx = __builtin_amdgcn_readfirstlane(
@@ -402,7 +401,6 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     if (__builtin_amdgcn_readfirstlane(won)) {
       issue_page(nx);
       pending = nx;
-      pending_since = ui;
     }
   };
   auto mark_ready = [&]() {
@@ -507,13 +505,10 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   };
 
   for (int ui = 0; ui < n_union; ++ui) {
-    try_claim(ui);
-    if (pending >= 0 && pending_since < ui) mark_ready();
     if (!is_ready(ui)) {
       // Bounded wait (the protocol cannot deadlock; the bound only guarantees
       // that a wave always finishes).
       for (int spin = 0; spin < (1 << 22); ++spin) {
-        mark_ready();
         try_claim(ui);
         mark_ready();
         if (is_ready(ui)) break;
@@ -529,7 +524,6 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       __hip_atomic_fetch_add(&s_done[ui % LS_ATT_STAGES], 1u, __ATOMIC_RELEASE,
                              __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  mark_ready();
 
   // ---- epilogue ----
 #pragma unroll
