@@ -299,6 +299,27 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   for (int i = 0; i < LS_ATT_WAVES; ++i) n_union += s_wsum[i];
   const int32_t* vexp_seq = vexp + (int64_t)g * n_pages_ws + pg_off[b];
   const float inv_scale_log2 = 1.f / scale_log2;
+  // The pages are visited in a strided order (ascending page i goes to slot
+  // i * stride mod n_union, a bijection for stride coprime to n_union):
+  // neighbouring pages tend to be selected by the same rows, and spreading
+  // them out evens the work of the waves over any window of pages.
+  // (Empty or one-page lists keep stride 1; a coprime odd stride below 64 + 7
+  // exists for any list this kernel accepts, the loop bound only caps it.)
+  int stride = 1;
+  if (n_union > 1) {
+    for (int cand = 7; cand < 71; cand += 2) {
+      int a = cand, b = n_union;
+      while (b) {
+        const int t = a % b;
+        a = b;
+        b = t;
+      }
+      if (a == 1) {
+        stride = cand;
+        break;
+      }
+    }
+  }
   while (word) {
     const int bit = __ffs(word) - 1;
     word &= word - 1;
@@ -306,9 +327,11 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     uint32_t rows = 0u;
 #pragma unroll
     for (int i = 0; i < LS_ATT_TILE; ++i) rows |= ((s_bits[i][tid] >> bit) & 1u) << i;
-    s_uexp[pos] = (int8_t)vexp_seq[page];
-    s_umask[pos] = rows;
-    s_union[pos++] = (uint16_t)page;
+    const int dst = (int)(((uint32_t)pos * (uint32_t)stride) % (uint32_t)n_union);
+    s_uexp[dst] = (int8_t)vexp_seq[page];
+    s_umask[dst] = rows;
+    s_union[dst] = (uint16_t)page;
+    ++pos;
   }
 
   // ---- per-row state: Q^T fragments (B operand), softmax stats, O^T ----
@@ -357,28 +380,43 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   const uint32_t ring_off = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(ls_lds_void*)s_ring);
   const int64_t k_rs_bytes = 2 * k_rs;
+  // Lane parts of the copy offsets (page-independent): K copy i covers rows
+  // 4i..4i+3, so R & 15 = 4 (i & 3) + l4 and the key is kbase(i) + l4; V^T copy
+  // i covers rows 8i..8i+7, so (d >> 1) & 7 = 4 (i & 1) + l4.  The i-dependent
+  // row offsets go into the scalar base.
+  const int l4 = lane >> 4;
+  uint32_t k_lane[4], v_lane[2];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    k_lane[m] = (uint32_t)(l4 * k_rs_bytes) + 16u * (uint32_t)((lane & 15) ^ (4 * m + l4));
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+    v_lane[m] = (uint32_t)((lane >> 3) * 2 * lpad) + 16u * (uint32_t)((lane & 7) ^ (4 * m + l4));
   auto issue_page = [&](int ui_copy) {
     const int page = __builtin_amdgcn_readfirstlane((int)s_union[ui_copy]);
     const uint32_t kb = ring_off + (ui_copy % LS_ATT_STAGES) * LS_ATT_STAGE_BYTES;
     const uint32_t vb = kb + LS_ATT_KBYTES;
     // Keys past the sequence end repeat its last key (their scores are masked).
     const int key_rem = lk - 1 - 64 * page;  // >= 0: every union page is visible
-    const int key_lim = key_rem < 63 ? key_rem : 63;
     const uint16_t* kpage = kgrp + (kstart + 64LL * page) * k_rs;
+    if (key_rem >= 63) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int R = 4 * i + (lane >> 4);
-      const int C = (lane & 15) ^ (R & 15);
-      const uint32_t voff = (uint32_t)(min(ls_att_key_of_row(R), key_lim) * k_rs_bytes) + 16u * C;
-      ls_dma16(kpage, voff, kb + i * 1024);
+      for (int i = 0; i < 16; ++i) {
+        const int kbase = 32 * (i >> 3) + 8 * (i & 3) + 4 * ((i >> 2) & 1);
+        ls_dma16(kpage + (int64_t)kbase * k_rs, k_lane[i & 3], kb + i * 1024);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kbase = 32 * (i >> 3) + 8 * (i & 3) + 4 * ((i >> 2) & 1);
+        const int key = min(kbase + l4, key_rem);
+        const uint32_t voff = (uint32_t)(key * k_rs_bytes) + (k_lane[i & 3] - (uint32_t)(l4 * k_rs_bytes));
+        ls_dma16(kpage, voff, kb + i * 1024);
+      }
     }
     const uint16_t* vpage = vgrp + 64LL * page;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int d = 8 * i + (lane >> 3);
-      const int C = (lane & 7) ^ ((d >> 1) & 7);
-      ls_dma16(vpage, (uint32_t)(d * 2 * lpad) + 16u * C, vb + i * 1024);
-    }
+    for (int i = 0; i < 16; ++i) ls_dma16(vpage + 8LL * i * lpad, v_lane[i & 1], vb + i * 1024);
   };
   int pending = -1;  // union index this wave copied and has not marked ready
   auto try_claim = [&](int ui) {
@@ -441,8 +479,10 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       }
       // V^T row 16 db + r (so (row >> 1) & 7 == (r >> 1) & 7), logical chunk 4c + q.
       const uint8_t* vrow = vb + r * 128 + (((4 * c + q) ^ ((r >> 1) & 7)) << 4);
+      if constexpr (LS_ATT_TPW > 1) {
 #pragma unroll
-      for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
+        for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
+      }
       const int key0 = base + 8 * q;
       // S^T of one row: lane (r, q) gets head r's raw scores of keys base + 8q + 0..7.
       auto qk = [&](int j, ls_f32x4& s0, ls_f32x4& s1) {
@@ -491,6 +531,10 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
                                 __builtin_amdgcn_exp2f(fmaf(sv[2 * i + 1], scale_log2, bias)));
         const float lsum = ls_sum_f16x2(pf[3], ls_sum_f16x2(pf[2], ls_sum_f16x2(pf[1], ls_sum_f16x2(pf[0], 0.f))));
         l_run[j] = fmaf(lsum, p_unscale, l_run[j]);
+        if constexpr (LS_ATT_TPW == 1) {  // one row: V^T fragments are read where they are used
+#pragma unroll
+          for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
+        }
 #pragma unroll
         for (int db = 0; db < 8; ++db) o[j][db] = LsElem<LS_F16>::mfma(vf[db], pf, o[j][db]);
       };
