@@ -33,6 +33,11 @@ WORKLOADS = {
     "minicpm41_8b_layer_ragged_8k_24k_48k_96k": dict(seq_lens=(8192, 24576, 49152, 98304)),
 }
 HBM_PEAK_GBS = 8000.0
+COPY_PROBE_BYTES = 1 << 30
+# HBM bytes per launch of the attention kernel, from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE runs of `bench.py --traffic-probe`, each scaled by what the same
+# counter reads for the probe's 1 GiB copy (see profiles/).
+TRAFFIC_FILE = ROOT / "profiles" / "attention_traffic.json"
 BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -69,6 +74,15 @@ def selection_flops(case, D: int = 128, F: int = 128) -> float:
             rows = min(64, n - 64 * qb)
             atom_dots += rows * max(0, hi - lo + 1)
     return total + 2.0 * G * F * atom_dots
+
+
+def _traffic(workload: str):
+    """Measured HBM bytes per attention launch for this workload, if recorded."""
+    try:
+        rec = json.loads(TRAFFIC_FILE.read_text())
+        return rec[workload]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def _event_ms(fn, iters: int) -> float:
@@ -129,6 +143,8 @@ def main() -> None:
     ap.add_argument("--kernel-iters", type=int, default=5)
     ap.add_argument("--cpu-rows-per-seq", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run one plain copy of COPY_PROBE_BYTES and one step, untimed (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path runs on a single device "
@@ -151,6 +167,19 @@ def main() -> None:
         kc, cu_c = compress_k(case.k, cu, cu_seqlens_host=cu_host)
         ids = leanselect_prefill_topk_idx(case.q, kc, cu, cu_c, case.selector, **kw)
         return sparse_attention(case.q, case.k, case.v, cu, cu, max_len, max_len, ids), ids
+
+    if args.traffic_probe:
+        # A plain device copy of known size calibrates the byte counters; then
+        # one step of the workload.
+        src = torch.empty(COPY_PROBE_BYTES // 2, dtype=torch.int16, device=dev).random_()
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        step()
+        torch.cuda.synchronize()
+        print(f"[bench] traffic probe done (copy of {COPY_PROBE_BYTES} bytes, one step)", file=sys.stderr)
+        return
 
     for _ in range(args.warmup):
         step()
@@ -205,7 +234,7 @@ def main() -> None:
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": _traffic(args.workload),
             "algorithmic_flops": attn_flops,
             "avg_keys_per_row": round(n_keys / (G * N), 1),
         },

@@ -151,6 +151,21 @@ def test_attention_messy_ids_duplicates_unsorted_out_of_range():
     _check_attention(case, messy.to(DEV), rows)
 
 
+def test_attention_union_sizes_with_small_factors():
+    """Tiles whose union has 1, 2, 7, 14, 21, 35 or 49 pages (the visit order is a
+    stride permutation of the union, which must stay a bijection for every size)."""
+    case, ids = _attention_case(lens=(4096,), seed=10)
+    G, N, T = ids.shape
+    crafted = torch.full((G, N, T), -1, dtype=torch.int32)
+    sizes = [1, 2, 7, 14, 21, 35, 49]
+    for t in range(N):
+        k = sizes[(t // 16) % len(sizes)]
+        pages = [p for p in range(k) if p <= t // 64][:T]
+        crafted[:, t, : len(pages)] = torch.tensor(pages, dtype=torch.int32)
+    rows = spread_rows(case.cu_host, per_seq=64)
+    _check_attention(case, crafted.to(DEV), rows)
+
+
 def test_attention_group_size_4_and_non_causal():
     case = workloads.head_space_layer(1024, device=DEV, dtype=torch.bfloat16)
     _, _, ids = _select(case)
