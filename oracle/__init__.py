@@ -10,3 +10,4 @@ here.
 
 from .leanselect_oracle import *  # noqa: F401,F403
 from .check import *  # noqa: F401,F403
+from .nosa_oracle import *  # noqa: F401,F403

@@ -1,0 +1,139 @@
+"""Pins the NOSA oracle (CPU): CIS pooling against the reference's own
+``avg_pool1d`` check, page pooling against LeanSelect's 5-atom page max and a
+brute-force loop, the two-stage selection against a loop restatement, and the
+one-pass attention against the reference's numerator / denominator form."""
+import math
+
+import pytest
+import torch
+
+import oracle
+
+
+def _cu(lens):
+    return torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0).tolist()), dtype=torch.int32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_mean_pooling_matches_avg_pool1d(dtype):
+    # The reference's self-test (cis_pooling.py:75-103): lens 67 and 1432, H 4,
+    # against avg_pool1d per sequence, broadcast to the sequence's rows.
+    torch.manual_seed(0)
+    lens = [67, 1432]
+    cu = _cu(lens)
+    N, H = sum(lens), 4
+    cis = torch.randn(N, H).to(dtype)
+    got = oracle.nosa_mean_pooling(cis, cu, max(lens))
+    M = max(lens) // 16 - 1
+    assert got.shape == (H, N, M)
+    want = torch.zeros(H, N, M, dtype=torch.float64)
+    for b in range(2):
+        s, e = int(cu[b]), int(cu[b + 1])
+        pooled = torch.nn.functional.avg_pool1d(cis[s:e].T.unsqueeze(0).double(), 32, 16)[0]
+        want[:, s:e, : pooled.shape[-1]] = pooled[:, None, :]
+    assert torch.equal(got, want.to(dtype))
+
+
+def _pool_loop(row, lk, out_len, off_bq, init, local):
+    out = []
+    for p in range(out_len):
+        if p < init or (off_bq - local <= p <= off_bq):
+            out.append(math.inf)
+            continue
+        vals = [row[j] for j in range(4 * p - 1, 4 * p + 4) if 0 <= j < lk]
+        out.append(max(vals) if vals else -math.inf)
+    return out
+
+
+def test_page_pooling_brute_force_and_leanselect_window():
+    torch.manual_seed(1)
+    lens_q, lens_k = [70, 300, 5], [3, 17, 0]  # compressed key counts
+    cq, ck = _cu(lens_q), _cu(lens_k)
+    Hk, T, max_k = 2, sum(lens_q), max(lens_k)
+    inp = torch.randn(Hk, T, max_k, dtype=torch.float64)
+    cache = torch.tensor([0, 64, 3])
+    got = oracle.page_maxpool_varlen(inp, cq, ck, cache, max(lens_q), max_k, local_blocks=2,
+                                     init_blocks=1)
+    out_len = (max(lens_q) + 64 + 63) // 64
+    assert got.shape == (Hk, T, out_len)
+    for b in range(3):
+        for t in range(int(cq[b]), int(cq[b + 1])):
+            off_bq = (t - int(cq[b]) + int(cache[b])) // 64
+            for h in range(Hk):
+                want = _pool_loop(inp[h, t].tolist(), lens_k[b], out_len, off_bq, 1, 2)
+                assert got[h, t].tolist() == want
+    # Non-forced pages pool exactly like LeanSelect's page max (pages.py:146-187).
+    row = inp[0, 100]
+    ls = oracle.pool_atoms_to_pages(row[: lens_k[1]], seq_len=64 * out_len)
+    p = oracle.page_maxpool_varlen(inp[:, 100:101], torch.tensor([0, 1]), torch.tensor([0, lens_k[1]]),
+                                   torch.tensor([0]), 64 * out_len, max_k, local_blocks=0, init_blocks=0)
+    free = [j for j in range(out_len) if j != 0]  # page 0 is the row's own (forced) page
+    assert torch.equal(p[0, 0, free], ls[free])
+
+
+def _select_loop(block_row, cis_row, q_idx, topk, n_short):
+    out_len = len(block_row)
+    order_qk = sorted(range(out_len), key=lambda p: (-block_row[p], p))
+    short = set(order_qk[: min(n_short, out_len)])
+    cis = [(-math.inf if p > q_idx else cis_row[p]) for p in range(out_len)]
+    cis = [math.inf if p in short else c for p, c in enumerate(cis)]
+    order = sorted(range(out_len), key=lambda p: (-cis[p], p))[: min(topk, out_len)]
+    ids = sorted(order)
+    return [(-1 if p > q_idx else p) for p in ids]
+
+
+def test_nosa_selection_loop_restatement():
+    torch.manual_seed(2)
+    lens = [700, 131]
+    cq = _cu(lens)
+    ck = _cu([(n - 32) // 16 + 1 for n in lens])
+    G, max_kc = 2, int((ck[1:] - ck[:-1]).max())
+    atom = torch.randn(G, sum(lens), max_kc).to(torch.bfloat16).double()
+    for b in range(2):
+        atom[:, int(cq[b]) : int(cq[b + 1]), int(ck[b + 1] - ck[b]):] = float("-inf")
+    cis = torch.randn(sum(lens), G).to(torch.bfloat16)
+    ids, block, over = oracle.nosa_select_prefill(
+        atom, cis, cq, ck, cq, max(lens), max(lens), topk=12, init_blocks=1, local_blocks=2,
+        select_blocks=3, return_scores=True)
+    q_idx = oracle.nosa_q_idx(cq, max(lens))
+    score_cis = oracle.nosa_mean_pooling(cis, cq, max(lens))
+    out_len = (max(lens) + 63) // 64
+    for r in range(0, sum(lens), 7):
+        b = 0 if r < lens[0] else 1
+        lk = int(ck[b + 1] - ck[b])
+        off = (r - int(cq[b])) // 64
+        for g in range(G):
+            brow = _pool_loop(atom[g, r].tolist(), lk, out_len, off, 1, 2)
+            crow = _pool_loop(score_cis[g, r].double().tolist(), lk, out_len, off, 1, 2)
+            want = _select_loop(brow, crow, int(q_idx[r]), 12, 1 + 2 + 3)
+            assert ids[g, r].tolist() == want, (r, g)
+
+
+def test_nosa_attention_is_numerator_over_denominator():
+    torch.manual_seed(3)
+    lens = [300, 90]
+    cq = _cu(lens)
+    N, H, G, D = sum(lens), 4, 2, 16
+    q, k, v = (torch.randn(N, n, D, dtype=torch.float64) for n in (H, G, G))
+    cis = torch.randn(N, G, dtype=torch.float64)
+    T = 3
+    ids = torch.full((G, N, T), -1, dtype=torch.int32)
+    for t in range(N):
+        b = 0 if t < lens[0] else 1
+        qp = (t - int(cq[b])) // 64
+        pages = sorted({0, qp, max(qp - 2, 0)})
+        ids[:, t, : len(pages)] = torch.tensor(pages, dtype=torch.int32)
+    got = oracle.nosa_attention(q, k, v, cis, cq, cq, ids, block_size=64)
+    w = torch.exp(cis)
+    num, _ = oracle.sparse_attention(q, k, v * w[:, :, None], cq, cq, ids)
+    den, _ = oracle.sparse_attention(q, k, w[:, :, None].expand(N, G, D).contiguous(), cq, cq, ids)
+    torch.testing.assert_close(got, num / den[..., :1], rtol=1e-12, atol=1e-12)
+
+
+def test_q_idx_is_aligned_to_the_longest_sequence():
+    # nosa.py:1175-1189: rows of a shorter sequence are shifted to end with the
+    # longest one (a property of the reference kept as is).
+    q = oracle.nosa_q_idx(_cu([70, 131]), 131)
+    assert q[:4].tolist() == [0, 0, 0, 1]          # (t + 61) // 64
+    assert q[69].item() == (69 + 61) // 64 == 2
+    assert q[70:72].tolist() == [0, 0] and q[-1].item() == 130 // 64
