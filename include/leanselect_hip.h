@@ -194,6 +194,104 @@ int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const void* k,
                           int32_t causal, void* out, float* lse, void* workspace,
                           size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* NOSA variant (leanselect/models/nosa.py, --method leanselect)             */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * CIS mean pooling: out[h, t, m] = mean of cis[cu_seqlens[b] + 16 m + i, h]
+ * over i < 32 for every row t of sequence b when 16 m + 32 <= len(b), else 0.
+ *   cis [total_n, num_heads] (rows cis_row_stride elements apart);
+ *   out [num_heads, total_n, out_cols] contiguous, out_cols = max_seqlen / 16 - 1.
+ * Sums in float32, rounded once to dtype.  kernel_size 32, stride 16 only.
+ * Replaces nosa_mean_pooling (leanselect/ops/cis_pooling.py:8-72).
+ */
+int ls_cis_mean_pool(const void* cis, int64_t cis_row_stride, int64_t total_n,
+                     int32_t num_heads, const int32_t* cu_seqlens, int32_t batch,
+                     int32_t max_seqlen, int32_t kernel_size, int32_t stride, int32_t dtype,
+                     void* out, int32_t out_cols, void* stream);
+
+/*
+ * Varlen page max-pool with the forced overlay:
+ *   input [num_heads, total_q, max_seqlen_k] -> out [num_heads, total_q, out_len].
+ * Row t of sequence b has page off = (t - cu_seqlens_q[b] + cache_lens[b]) /
+ * block_size.  Page p is +inf when p < init_blocks or off - local_blocks <= p
+ * <= off, else the max of input[h, t, j] over j in [p s - 1, p s + s) clipped
+ * to [0, min(cu_seqlens_k[b + 1] - cu_seqlens_k[b], max_seqlen_k)) (-inf when
+ * empty), s = block_size / stride.
+ * Replaces infllm_v2.max_pooling_1d_varlen (third_party/infllmv2/paper1.patch:2664-2760,
+ * called at leanselect/models/nosa.py:1263-1286).
+ */
+int ls_page_maxpool_varlen(const void* input, const int32_t* cu_seqlens_q,
+                           const int32_t* cu_seqlens_k, const int32_t* cache_lens, int32_t batch,
+                           int32_t num_heads, int64_t total_q, int64_t max_seqlen_k,
+                           int64_t out_len, int32_t local_blocks, int32_t init_blocks,
+                           int32_t block_size, int32_t stride, int32_t dtype, void* out,
+                           void* stream);
+
+/*
+ * Workspace bytes needed by ls_nosa_select_prefill (max_pages =
+ * ceil(max_seqlen_q / block_size)).
+ */
+size_t ls_nosa_select_workspace_size(int64_t total_q, int64_t total_atoms, int32_t batch,
+                                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t router_heads, int32_t router_dim,
+                                     int32_t max_pages, int32_t dtype);
+
+/*
+ * NOSA prefill page plans, the LeanSelect branch of compressed_attention:
+ *   1. qk page scores: the folded-router atom scores (as ls_select_prefill),
+ *      max-pooled to pages with sink and local pages +inf, no causal mask;
+ *   2. the min(init + local + select, out_len) best qk pages (ties to the
+ *      lower page) form a shortlist;
+ *   3. CIS page scores: CIS window means (cis [total_k, num_kv_heads], rows
+ *      cis_row_stride apart, of cis_dtype; windows of sequence b per
+ *      cu_seqlens_k) max-pooled to pages, sink/local pages +inf, pages after
+ *      q_idx -inf, shortlisted pages +inf;
+ *   4. topk_idx [num_kv_heads, total_q, take] int32: the take = min(topk,
+ *      out_len) best pages, ascending, ids after q_idx replaced by -1.
+ * out_len = ceil(max_seqlen_q / block_size); q_idx = (t - cu_seqlens_q[b] +
+ * max_seqlen_q - len_q(b)) / block_size.  block_size 64, kernel_stride 16.
+ * Replaces compressed_attention(..., precomputed_qk_score=...) with
+ * _leanselect_atom_scores (leanselect/models/nosa.py:1144-1307, 1822-1853).
+ */
+int ls_nosa_select_prefill(const void* q, int64_t q_row_stride, int64_t total_q, const void* kc,
+                           int64_t kc_row_stride, int64_t total_atoms, const void* cis,
+                           int64_t cis_row_stride, int32_t cis_dtype,
+                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kc,
+                           const int32_t* cu_seqlens_k, int32_t batch, int32_t max_seqlen_q,
+                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                           const float* head_mix, const float* kv_head_mix, const float* q_proj,
+                           const float* k_proj, int32_t router_heads, int32_t router_dim,
+                           int32_t dtype, int32_t topk, int32_t block_size,
+                           int32_t kernel_stride, int32_t init_blocks, int32_t local_blocks,
+                           int32_t select_blocks, int32_t* topk_idx, int32_t take,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes needed by ls_nosa_attn_varlen.
+ */
+size_t ls_nosa_attn_workspace_size(int64_t total_k, int32_t batch, int32_t num_kv_heads,
+                                   int32_t head_dim, int32_t max_seqlen_k, int32_t dtype);
+
+/*
+ * NOSA attention: ls_sparse_attn_varlen (causal) with a per-key bias,
+ *   out[t, h] = sum_j w_j v[j] / sum_j w_j,  w_j = exp(scale * q[t, h] . k[j] + cis[j, g]),
+ * the closed form of attn(q, k, v * e^cis) / attn(q, k, e^cis) (both through
+ * infllmv2_attn_varlen_func at leanselect/models/nosa.py:2211-2255) in one
+ * pass.  cis [total_k, num_kv_heads] of cis_dtype (finite), rows
+ * cis_row_stride apart.  lse (optional) is the log of sum_j w_j.
+ */
+int ls_nosa_attn_varlen(const void* q, int64_t q_row_stride, const void* k, int64_t k_row_stride,
+                        const void* v, int64_t v_row_stride, const void* cis,
+                        int64_t cis_row_stride, int32_t cis_dtype, const int32_t* cu_seqlens_q,
+                        const int32_t* cu_seqlens_k, int32_t batch, int64_t total_q,
+                        int64_t total_k, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                        const int32_t* topk_idx, int32_t take, int32_t block_size,
+                        float softmax_scale, void* out, float* lse, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -44,6 +44,21 @@ SIGNATURES = {
     "ls_sparse_attn_varlen": (
         _i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _i32, _i64, _i64, _i32, _i32, _i32, _i32,
                _i32, _i32, _p, _i32, _i32, _f32, _i32, _p, _p, _p, _sz, _p]),
+    "ls_cis_mean_pool": (
+        _i32, [_p, _i64, _i64, _i32, _p, _i32, _i32, _i32, _i32, _i32, _p, _i32, _p]),
+    "ls_page_maxpool_varlen": (
+        _i32, [_p, _p, _p, _p, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p,
+               _p]),
+    "ls_nosa_select_workspace_size": (
+        _sz, [_i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "ls_nosa_select_prefill": (
+        _i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _p, _i32, _i32, _i32,
+               _i32, _i32, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+               _p, _i32, _p, _sz, _p]),
+    "ls_nosa_attn_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32]),
+    "ls_nosa_attn_varlen": (
+        _i32, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32, _p, _p, _i32, _i64, _i64, _i32,
+               _i32, _i32, _i32, _i32, _i32, _p, _i32, _i32, _f32, _p, _p, _p, _sz, _p]),
 }
 
 _lib = None

@@ -1,4 +1,4 @@
-// Block-sparse causal attention over per-token page plans (a10).
+// Block-sparse causal attention over per-token page plans.
 //
 // Contract: infllmv2_attn_varlen_func(..., topk_idx=)
 // (third_party/infllmv2/paper1.patch:1993-2100; called from
@@ -200,11 +200,14 @@ __device__ __forceinline__ float ls_sum_f16x2(uint32_t x, float acc) {
 #define LS_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt(((n) & 0xf) | (((n) >> 4) << 14) | (0x7 << 4) | (0xf << 8))
 
-template <int DT>
+// BIAS adds a per-key score bias (the NOSA eviction score, pre-scaled to base
+// 2): weight_j = 2^(scale_log2 * q.k_j + cb_j).  cb[g][64 pg_off[b] + j] is
+// staged like V^T and copied with each page (256 B per stage).
+template <int DT, bool BIAS>
 __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_tile_kernel(
     const uint16_t* __restrict__ qg, int64_t q_rs, const uint16_t* __restrict__ kg,
     int64_t k_rs, const uint16_t* __restrict__ vt, int64_t lpad,
-    const int32_t* __restrict__ vexp, int64_t n_pages_ws,
+    const int32_t* __restrict__ vexp, const float* __restrict__ cb, int64_t n_pages_ws,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
     const int32_t* __restrict__ pg_off, const int32_t* __restrict__ tile_off, int batch,
     int64_t total_q, int G, int gs, const int32_t* __restrict__ topk_idx, int take,
@@ -223,6 +226,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   // s_ready[st] = union index + 1 of the page whose copy into stage st has
   // landed; s_done[st] = waves finished with stage st, over all its pages.
   __shared__ uint32_t s_next, s_ready[LS_ATT_STAGES], s_done[LS_ATT_STAGES];
+  __shared__ __align__(16) float s_bias[BIAS ? LS_ATT_STAGES * 64 : 4];
   static_assert(LS_ATT_TILE * LS_ATT_WORDS * 4 <= LS_ATT_STAGES * LS_ATT_STAGE_BYTES,
                 "page bitmaps must fit in the ring");
   static_assert(LS_ATT_TILE <= 32, "row masks are 32-bit");
@@ -377,6 +381,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   // depends only on pages that are marked or being copied by a waiting wave.
   const uint16_t* kgrp = kg + (int64_t)g * D;
   const uint16_t* vgrp = vt + (int64_t)g * D * lpad + vbase;
+  const float* cgrp = BIAS ? cb + (int64_t)g * lpad + vbase : nullptr;
+  ls_u32x4 pending_cb = {0u, 0u, 0u, 0u};  // bias of the page being copied (lanes 0..15)
   const uint32_t ring_off = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(ls_lds_void*)s_ring);
   const int64_t k_rs_bytes = 2 * k_rs;
@@ -417,6 +423,9 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     const uint16_t* vpage = vgrp + 64LL * page;
 #pragma unroll
     for (int i = 0; i < 16; ++i) ls_dma16(vpage + 8LL * i * lpad, v_lane[i & 1], vb + i * 1024);
+    // The page's 64 biases go through registers (stored to LDS once landed).
+    if constexpr (BIAS)
+      if (lane < 16) pending_cb = *reinterpret_cast<const ls_u32x4*>(cgrp + 64LL * page + 4 * lane);
   };
   int pending = -1;  // union index this wave copied and has not marked ready
   auto try_claim = [&](int ui) {
@@ -444,6 +453,9 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   auto mark_ready = [&]() {
     if (pending < 0) return;
     LS_WAIT_VMCNT(0);  // this wave's copies are its only outstanding loads
+    if constexpr (BIAS)
+      if (lane < 16)
+        *reinterpret_cast<ls_u32x4*>(s_bias + (pending % LS_ATT_STAGES) * 64 + 4 * lane) = pending_cb;
     if (lane == 0)
       __hip_atomic_store(&s_ready[pending % LS_ATT_STAGES], (uint32_t)pending + 1u,
                          __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -484,6 +496,12 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
         for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
       }
       const int key0 = base + 8 * q;
+      ls_f32x4 cbv0, cbv1;  // this lane's eight key biases (BIAS only)
+      if constexpr (BIAS) {
+        const float* bp = s_bias + (ui % LS_ATT_STAGES) * 64 + 32 * c + 8 * q;
+        cbv0 = *reinterpret_cast<const ls_f32x4*>(bp);
+        cbv1 = *reinterpret_cast<const ls_f32x4*>(bp + 4);
+      }
       // S^T of one row: lane (r, q) gets head r's raw scores of keys base + 8q + 0..7.
       auto qk = [&](int j, ls_f32x4& s0, ls_f32x4& s1) {
         s0 = ls_f32x4{0.f, 0.f, 0.f, 0.f};
@@ -502,6 +520,15 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
           for (int i = 0; i < 8; ++i)
             if (key0 + i > jmax_r[j]) sv[i] = -INFINITY;
         }
+        // With a bias the scores are taken to base-2 units here (thr, m_run
+        // and the maxima below are then all in those units).
+        if constexpr (BIAS) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            sv[i] = fmaf(sv[i], scale_log2, cbv0[i]);
+            sv[4 + i] = fmaf(sv[4 + i], scale_log2, cbv1[i]);
+          }
+        }
         // Plain maxima: the compiler inserts the wait states an MFMA result
         // needs before a VALU read (it cannot for inline asm), and this file is
         // built without IEEE NaN quieting, so they fuse into v_max3.
@@ -513,10 +540,10 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
           float cm = lmax;
           cm = fmaxf(cm, ls_shfl_xor(cm, 16));
           cm = fmaxf(cm, ls_shfl_xor(cm, 32));
-          const float m_new = fmaxf(m_run[j], cm * scale_log2);
+          const float m_new = fmaxf(m_run[j], BIAS ? cm : cm * scale_log2);
           const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
           m_run[j] = m_new;
-          thr[j] = (m_new + 8.f) * inv_scale_log2;
+          thr[j] = BIAS ? m_new + 8.f : (m_new + 8.f) * inv_scale_log2;
           l_run[j] *= alpha;
 #pragma unroll
           for (int db = 0; db < 8; ++db) o[j][db] *= alpha;
@@ -526,9 +553,14 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
         const float bias = (float)v_e - m_run[j];
         ls_u32x4 pf;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          pf[i] = ls_pack_f16x2(__builtin_amdgcn_exp2f(fmaf(sv[2 * i], scale_log2, bias)),
-                                __builtin_amdgcn_exp2f(fmaf(sv[2 * i + 1], scale_log2, bias)));
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (BIAS)
+            pf[i] = ls_pack_f16x2(__builtin_amdgcn_exp2f(sv[2 * i] + bias),
+                                  __builtin_amdgcn_exp2f(sv[2 * i + 1] + bias));
+          else
+            pf[i] = ls_pack_f16x2(__builtin_amdgcn_exp2f(fmaf(sv[2 * i], scale_log2, bias)),
+                                  __builtin_amdgcn_exp2f(fmaf(sv[2 * i + 1], scale_log2, bias)));
+        }
         const float lsum = ls_sum_f16x2(pf[3], ls_sum_f16x2(pf[2], ls_sum_f16x2(pf[1], ls_sum_f16x2(pf[0], 0.f))));
         l_run[j] = fmaf(lsum, p_unscale, l_run[j]);
         if constexpr (LS_ATT_TPW == 1) {  // one row: V^T fragments are read where they are used
@@ -591,15 +623,35 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   }
 }
 
+// NOSA key biases: cb[g][64 pg_off[b] + j] = log2(e) * cis[cu_k[b] + j][g] for
+// j < len_k(b), 0 past each sequence end (those keys are never visible).  One
+// workgroup per 64-key page of one group.
+template <int CT>
+__global__ __launch_bounds__(64) void ls_bias_kernel(const typename LsElem<CT>::T* __restrict__ cis,
+                                                     int64_t cis_rs, const int32_t* __restrict__ cu_k,
+                                                     const int32_t* __restrict__ pg_off, int batch,
+                                                     int64_t lpad, float* __restrict__ cb) {
+  const int64_t tile_id = LS_BID_X;
+  if (tile_id >= pg_off[batch]) return;
+  const int g = LS_BID_Y;
+  const int b = ls_find_segment(pg_off, batch, tile_id);
+  const int p = (int)(tile_id - pg_off[b]);
+  const int lk = cu_k[b + 1] - cu_k[b];
+  const int j = 64 * p + LS_TID;
+  float v = 0.f;
+  if (j < lk) v = LsElem<CT>::to_f(cis[((int64_t)cu_k[b] + j) * cis_rs + g]) * 1.4426950408889634f;
+  cb[(int64_t)g * lpad + 64LL * (pg_off[b] + p) + LS_TID] = v;
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 namespace {
 struct AttnWs {
-  size_t vt, pg, tiles, vexp, total;
+  size_t vt, pg, tiles, vexp, cb, total;
   int64_t lpad, n_pages;
 };
-AttnWs attn_ws(int64_t total_k, int batch, int G, int D, int eb) {
+AttnWs attn_ws(int64_t total_k, int batch, int G, int D, int eb, bool bias) {
   AttnWs L;
   L.n_pages = (total_k + 63) / 64 + batch;
   L.lpad = L.n_pages * 64;
@@ -608,61 +660,69 @@ AttnWs attn_ws(int64_t total_k, int batch, int G, int D, int eb) {
   L.pg = off; off += ls_align256((size_t)(batch + 1) * 4);
   L.tiles = off; off += ls_align256((size_t)(batch + 1) * 4);
   L.vexp = off; off += ls_align256((size_t)G * L.n_pages * 4);
+  L.cb = off; off += bias ? ls_align256((size_t)G * L.lpad * 4) : 0;
   L.total = off;
   return L;
 }
-}  // namespace
 
-extern "C" size_t ls_sparse_attn_workspace_size(int64_t total_k, int32_t batch,
-                                                int32_t num_kv_heads, int32_t head_dim,
-                                                int32_t max_seqlen_k, int32_t dtype) {
-  (void)max_seqlen_k;
-  return attn_ws(total_k, batch, num_kv_heads, head_dim, (int)ls_dtype_bytes(dtype)).total;
+template <int DT, bool BIAS>
+void launch_tile(dim3 grid, hipStream_t s, const void* q, int64_t q_rs, const void* k, int64_t k_rs,
+                 const uint16_t* vt, const AttnWs& L, const int32_t* vexp, const float* cb,
+                 const int32_t* cu_q, const int32_t* cu_k, const int32_t* pg,
+                 const int32_t* tiles, int batch, int64_t total_q, int G, int gs,
+                 const int32_t* topk_idx, int take, float scale_log2, int causal, void* out,
+                 float* lse) {
+  hipLaunchKernelGGL((ls_attn_tile_kernel<DT, BIAS>), grid, dim3(LS_ATT_THREADS), 0, s,
+                     (const uint16_t*)q, q_rs, (const uint16_t*)k, k_rs, vt, L.lpad, vexp, cb,
+                     L.n_pages, cu_q, cu_k, pg, tiles, batch, total_q, G, gs, topk_idx, take,
+                     scale_log2, causal, (uint16_t*)out, lse, (int)(grid.x / 8));
 }
 
-extern "C" int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const void* k,
-                                     int64_t k_row_stride, const void* v, int64_t v_row_stride,
-                                     const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                                     int32_t batch, int64_t total_q, int64_t total_k,
-                                     int32_t max_seqlen_q, int32_t max_seqlen_k,
-                                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                                     int32_t dtype, const int32_t* topk_idx, int32_t take,
-                                     int32_t block_size, float softmax_scale, int32_t causal,
-                                     void* out, float* lse, void* workspace,
-                                     size_t workspace_bytes, void* stream) {
+// Shared body of the plain and the NOSA (cis != nullptr) entry points.
+int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k,
+             int64_t k_row_stride, const void* v, int64_t v_row_stride, const void* cis,
+             int64_t cis_row_stride, int32_t cis_dtype, const int32_t* cu_seqlens_q,
+             const int32_t* cu_seqlens_k, int32_t batch, int64_t total_q, int64_t total_k,
+             int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+             int32_t dtype, const int32_t* topk_idx, int32_t take, int32_t block_size,
+             float softmax_scale, int32_t causal, void* out, float* lse, void* workspace,
+             size_t workspace_bytes, void* stream) {
+  const bool bias = cis != nullptr;
   LS_REQUIRE(dtype == LS_BF16 || dtype == LS_F16, LS_ERR_UNSUPPORTED,
-             "ls_sparse_attn_varlen: only bf16 and fp16 are supported (dtype %d)", dtype);
-  LS_REQUIRE(head_dim == 128, LS_ERR_UNSUPPORTED,
-             "ls_sparse_attn_varlen: head_dim must be 128 (got %d)", head_dim);
-  LS_REQUIRE(block_size == 64, LS_ERR_UNSUPPORTED,
-             "ls_sparse_attn_varlen: block_size must be 64 (got %d)", block_size);
+             "%s: only bf16 and fp16 are supported (dtype %d)", who, dtype);
+  LS_REQUIRE(head_dim == 128, LS_ERR_UNSUPPORTED, "%s: head_dim must be 128 (got %d)", who,
+             head_dim);
+  LS_REQUIRE(block_size == 64, LS_ERR_UNSUPPORTED, "%s: block_size must be 64 (got %d)", who,
+             block_size);
   LS_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0, LS_ERR_INVALID,
-             "ls_sparse_attn_varlen: num_heads must be a positive multiple of num_kv_heads");
+             "%s: num_heads must be a positive multiple of num_kv_heads", who);
   LS_REQUIRE(batch >= 0 && total_q >= 0 && total_k >= 0 && take >= 0, LS_ERR_INVALID,
-             "ls_sparse_attn_varlen: bad sizes");
-  LS_REQUIRE(take <= LS_ATTN_MAX_TAKE, LS_ERR_UNSUPPORTED,
-             "ls_sparse_attn_varlen: at most %d ids per row (got %d)", LS_ATTN_MAX_TAKE, take);
+             "%s: bad sizes", who);
+  LS_REQUIRE(take <= LS_ATTN_MAX_TAKE, LS_ERR_UNSUPPORTED, "%s: at most %d ids per row (got %d)",
+             who, LS_ATTN_MAX_TAKE, take);
   LS_REQUIRE((int64_t)max_seqlen_k <= 64LL * LS_ATTN_MAX_PAGES, LS_ERR_UNSUPPORTED,
-             "ls_sparse_attn_varlen: max_seqlen_k above %d", 64 * LS_ATTN_MAX_PAGES);
-  (void)max_seqlen_q;
+             "%s: max_seqlen_k above %d", who, 64 * LS_ATTN_MAX_PAGES);
+  LS_REQUIRE(!bias || cis_dtype == LS_F32 || cis_dtype == LS_BF16 || cis_dtype == LS_F16,
+             LS_ERR_INVALID, "%s: unknown CIS dtype %d", who, cis_dtype);
   if (total_q == 0 || batch == 0) return LS_OK;
   LS_REQUIRE(q && k && v && out && cu_seqlens_q && cu_seqlens_k && (take == 0 || topk_idx),
-             LS_ERR_INVALID, "ls_sparse_attn_varlen: null pointer");
+             LS_ERR_INVALID, "%s: null pointer", who);
   LS_REQUIRE(ls_aligned16(q) && ls_aligned16(k) && ls_aligned16(v) && ls_aligned16(out) &&
                  q_row_stride % 8 == 0 && k_row_stride % 8 == 0 && v_row_stride % 8 == 0,
              LS_ERR_UNSUPPORTED,
-             "ls_sparse_attn_varlen: tensors must be 16-byte aligned with row strides %% 8 == 0");
-  const AttnWs L = attn_ws(total_k, batch, num_kv_heads, head_dim, 2);
+             "%s: tensors must be 16-byte aligned with row strides %% 8 == 0", who);
+  const AttnWs L = attn_ws(total_k, batch, num_kv_heads, head_dim, 2, bias);
   LS_REQUIRE(L.lpad * 2 * head_dim < (1LL << 32) && 64LL * k_row_stride * 2 < (1LL << 31),
-             LS_ERR_UNSUPPORTED, "ls_sparse_attn_varlen: too many keys for 32-bit copy offsets");
+             LS_ERR_UNSUPPORTED, "%s: too many keys for 32-bit copy offsets", who);
   LS_REQUIRE(workspace && workspace_bytes >= L.total, LS_ERR_WORKSPACE,
-             "ls_sparse_attn_varlen: workspace needs %zu bytes", L.total);
+             "%s: workspace needs %zu bytes", who, L.total);
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   uint16_t* vt = (uint16_t*)(ws + L.vt);
   int32_t* pg = (int32_t*)(ws + L.pg);
   int32_t* vexp = (int32_t*)(ws + L.vexp);
   int32_t* tiles = (int32_t*)(ws + L.tiles);
+  float* cb = bias ? (float*)(ws + L.cb) : nullptr;
   hipLaunchKernelGGL(ls_attn_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens_q, cu_seqlens_k,
                      batch, LS_ATT_TILE, pg, tiles);
   int rc = ls_check_launch("ls_attn_plan_kernel");
@@ -676,23 +736,87 @@ extern "C" int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const 
       hipLaunchKernelGGL((ls_vt_kernel<LS_F16, 128>), vgrid, dim3(256), 0, s, (const uint16_t*)v,
                          v_row_stride, cu_seqlens_k, pg, batch, L.lpad, L.n_pages, vt, vexp);
     if ((rc = ls_check_launch("ls_vt_kernel"))) return rc;
+    if (bias) {
+      if (cis_dtype == LS_BF16)
+        hipLaunchKernelGGL(ls_bias_kernel<LS_BF16>, vgrid, dim3(64), 0, s, (const uint16_t*)cis,
+                           cis_row_stride, cu_seqlens_k, pg, batch, L.lpad, cb);
+      else if (cis_dtype == LS_F16)
+        hipLaunchKernelGGL(ls_bias_kernel<LS_F16>, vgrid, dim3(64), 0, s, (const uint16_t*)cis,
+                           cis_row_stride, cu_seqlens_k, pg, batch, L.lpad, cb);
+      else
+        hipLaunchKernelGGL(ls_bias_kernel<LS_F32>, vgrid, dim3(64), 0, s, (const float*)cis,
+                           cis_row_stride, cu_seqlens_k, pg, batch, L.lpad, cb);
+      if ((rc = ls_check_launch("ls_bias_kernel"))) return rc;
+    }
   }
   const int gs = num_heads / num_kv_heads;
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf((float)head_dim);
   const float scale_log2 = scale * 1.4426950408889634f;
   const int64_t tile_bound = (total_q + LS_ATT_TILE - 1) / LS_ATT_TILE + batch;
   const dim3 grid((unsigned)(8 * ((tile_bound + 7) / 8)), num_kv_heads, (gs + 15) / 16);
-  if (dtype == LS_BF16)
-    hipLaunchKernelGGL(ls_attn_tile_kernel<LS_BF16>, grid, dim3(LS_ATT_THREADS), 0, s, (const uint16_t*)q,
-                       q_row_stride, (const uint16_t*)k, k_row_stride, vt, L.lpad, vexp,
-                       L.n_pages, cu_seqlens_q, cu_seqlens_k, pg, tiles, batch, total_q,
-                       num_kv_heads, gs, topk_idx, take, scale_log2, causal, (uint16_t*)out, lse,
-                       (int)(grid.x / 8));
-  else
-    hipLaunchKernelGGL(ls_attn_tile_kernel<LS_F16>, grid, dim3(LS_ATT_THREADS), 0, s, (const uint16_t*)q,
-                       q_row_stride, (const uint16_t*)k, k_row_stride, vt, L.lpad, vexp,
-                       L.n_pages, cu_seqlens_q, cu_seqlens_k, pg, tiles, batch, total_q,
-                       num_kv_heads, gs, topk_idx, take, scale_log2, causal, (uint16_t*)out, lse,
-                       (int)(grid.x / 8));
+#define LS_TILE_ARGS                                                                              \
+  grid, s, q, q_row_stride, k, k_row_stride, vt, L, vexp, cb, cu_seqlens_q, cu_seqlens_k, pg,     \
+      tiles, batch, total_q, num_kv_heads, gs, topk_idx, take, scale_log2, causal, out, lse
+  if (dtype == LS_BF16) {
+    if (bias) launch_tile<LS_BF16, true>(LS_TILE_ARGS);
+    else launch_tile<LS_BF16, false>(LS_TILE_ARGS);
+  } else {
+    if (bias) launch_tile<LS_F16, true>(LS_TILE_ARGS);
+    else launch_tile<LS_F16, false>(LS_TILE_ARGS);
+  }
+#undef LS_TILE_ARGS
   return ls_check_launch("ls_attn_tile_kernel");
+}
+}  // namespace
+
+extern "C" size_t ls_sparse_attn_workspace_size(int64_t total_k, int32_t batch,
+                                                int32_t num_kv_heads, int32_t head_dim,
+                                                int32_t max_seqlen_k, int32_t dtype) {
+  (void)max_seqlen_k;
+  return attn_ws(total_k, batch, num_kv_heads, head_dim, (int)ls_dtype_bytes(dtype), false).total;
+}
+
+extern "C" size_t ls_nosa_attn_workspace_size(int64_t total_k, int32_t batch,
+                                              int32_t num_kv_heads, int32_t head_dim,
+                                              int32_t max_seqlen_k, int32_t dtype) {
+  (void)max_seqlen_k;
+  return attn_ws(total_k, batch, num_kv_heads, head_dim, (int)ls_dtype_bytes(dtype), true).total;
+}
+
+extern "C" int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const void* k,
+                                     int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                     const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                     int32_t batch, int64_t total_q, int64_t total_k,
+                                     int32_t max_seqlen_q, int32_t max_seqlen_k,
+                                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t dtype, const int32_t* topk_idx, int32_t take,
+                                     int32_t block_size, float softmax_scale, int32_t causal,
+                                     void* out, float* lse, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  (void)max_seqlen_q;
+  return attn_run("ls_sparse_attn_varlen", q, q_row_stride, k, k_row_stride, v, v_row_stride,
+                  nullptr, 0, 0, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k,
+                  max_seqlen_k, num_heads, num_kv_heads, head_dim, dtype, topk_idx, take,
+                  block_size, softmax_scale, causal, out, lse, workspace, workspace_bytes,
+                  stream);
+}
+
+extern "C" int ls_nosa_attn_varlen(const void* q, int64_t q_row_stride, const void* k,
+                                   int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                   const void* cis, int64_t cis_row_stride, int32_t cis_dtype,
+                                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                   int32_t batch, int64_t total_q, int64_t total_k,
+                                   int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads,
+                                   int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                                   const int32_t* topk_idx, int32_t take, int32_t block_size,
+                                   float softmax_scale, void* out, float* lse, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  (void)max_seqlen_q;
+  LS_REQUIRE(total_k == 0 || cis, LS_ERR_INVALID, "ls_nosa_attn_varlen: null CIS scores");
+  static const uint16_t kNoKeys = 0;  // any non-null pointer: no key reads it
+  return attn_run("ls_nosa_attn_varlen", q, q_row_stride, k, k_row_stride, v, v_row_stride,
+                  cis ? cis : &kNoKeys, cis_row_stride, cis_dtype, cu_seqlens_q, cu_seqlens_k,
+                  batch, total_q, total_k, max_seqlen_k, num_heads, num_kv_heads, head_dim,
+                  dtype, topk_idx, take, block_size, softmax_scale, 1, out, lse, workspace,
+                  workspace_bytes, stream);
 }

@@ -107,6 +107,21 @@ __device__ __forceinline__ float ls_shfl_xor(float v, int mask) {
   return __shfl_xor(v, mask, LS_WAVE);
 }
 
+// Order-preserving unsigned keys of 16-bit (bf16 / fp16) and float32 scores:
+// a > b as floats  <=>  key(a) > key(b) as integers (NaN aside).
+__host__ __device__ __forceinline__ uint32_t ls_order_key16(uint16_t b) {
+  return (b & 0x8000u) ? (~(uint32_t)b & 0xffffu) : ((uint32_t)b | 0x8000u);
+}
+__host__ __device__ __forceinline__ uint32_t ls_order_key32(uint32_t u) {
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Number of set bits of `mask` in the lanes below this one.
+__device__ __forceinline__ int ls_lanes_below(uint64_t mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
 // Index of the segment containing `x` in a nondecreasing prefix array
 // `off[0..n]` (off[0] == 0): largest b < n with off[b] <= x.
 __device__ __forceinline__ int ls_find_segment(const int32_t* off, int n, int64_t x) {

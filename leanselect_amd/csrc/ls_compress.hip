@@ -1,4 +1,4 @@
-// Compressed keys (a1): mean of kernel_size-token windows at kernel_stride,
+// Compressed keys: mean of kernel_size-token windows at kernel_stride,
 // per packed sequence.  HBM-bound; each thread owns 8 consecutive channels of
 // one (atom, kv-head) and sums its window in float32 in token order.
 //

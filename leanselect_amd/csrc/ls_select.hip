@@ -1,4 +1,4 @@
-// LeanSelect prefill selection on gfx950 (a2-a9).
+// LeanSelect prefill selection on gfx950.
 //
 //   fused weights  q_fused / kv_fused          leanselect/selector.py:144-158
 //   q~ = Q . q_fused summed over the GQA group leanselect/selector.py:160-177   (MFMA GEMM)
@@ -11,6 +11,7 @@
 // rounded to the activation dtype; a page score is the max of rounded atom
 // scores (rounding is monotone, so the max is rounded once).
 #include "ls_common.h"
+#include "ls_nosa_internal.h"
 
 // ---------------------------------------------------------------------------
 // Fused weights
@@ -242,11 +243,17 @@ __global__ void ls_select_plan_kernel(const int32_t* __restrict__ cu_q, int batc
 // the lane group below, one rotate away, or the carry from the previous step
 // for q == 0.
 //
-// SELECT: per sequence, only the non-forced visible pages
+// Modes (LS_SCORE_*): SELECT: per sequence, only the non-forced visible pages
 // [init_blocks, qp - local_blocks - 1] of the block are scored, into the
-// scratch rows P[g][t][*].  FULL: a single sequence, every page, out[g][n][*].
+// scratch rows P[g][t][*].  ALL: per sequence, every page whose window holds
+// an atom (p <= A_b / 4, below the page-column count), causal or not (the NOSA
+// shortlist ranks them all).  FULL: a single sequence, every page, out[g][n][*].
 // ---------------------------------------------------------------------------
-template <int DT, int KS, bool SELECT>
+#define LS_SCORE_FULL 0
+#define LS_SCORE_SELECT 1
+#define LS_SCORE_ALL 2
+
+template <int DT, int KS, int MODE>
 __global__ __launch_bounds__(256) void ls_score_mfma_kernel(
     const uint16_t* __restrict__ qt, int64_t Nq, const uint16_t* __restrict__ kt, int64_t Na,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_a,
@@ -259,17 +266,22 @@ __global__ __launch_bounds__(256) void ls_score_mfma_kernel(
 
   int64_t tq0, tq_end, a0, n_atoms;
   int p_lo, p_hi;
-  if constexpr (SELECT) {
+  if constexpr (MODE != LS_SCORE_FULL) {
     const int64_t ir = n_blk_launch - 1 - (int64_t)blockIdx.x;  // longest rows first
     if (ir >= blk_off[batch]) return;
     const int b = ls_find_segment(blk_off, batch, ir);
     const int qb = (int)(ir - blk_off[b]);
-    tq0 = (int64_t)cu_q[b] + 64LL * qb;
+    tq0 = (int64_t)cu_q[b] + (int64_t)64 * qb;
     tq_end = min(tq0 + 64, (int64_t)cu_q[b + 1]);
     a0 = cu_a[b];
     n_atoms = (int64_t)cu_a[b + 1] - a0;
-    p_lo = init_blocks;
-    p_hi = qb - local_blocks - 1;
+    if constexpr (MODE == LS_SCORE_SELECT) {
+      p_lo = init_blocks;
+      p_hi = qb - local_blocks - 1;
+    } else {  // full_seq_len carries the page-column count in this mode
+      p_lo = 0;
+      p_hi = (int)min(n_atoms / 4, full_seq_len - 1);
+    }
   } else {
     tq0 = 64LL * blockIdx.x;
     tq_end = min(tq0 + 64, Nq);
@@ -346,7 +358,7 @@ __global__ __launch_bounds__(256) void ls_score_mfma_kernel(
 
 // float32 page scores on the vector ALU: one thread per (group, token, page).
 // General pooling stride s = block_size / kernel_stride.
-template <bool SELECT>
+template <int MODE>
 __global__ __launch_bounds__(256) void ls_score_f32_kernel(
     const float* __restrict__ qt, int64_t Nq, const float* __restrict__ kt, int64_t Na, int F,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_a, int batch,
@@ -358,12 +370,17 @@ __global__ __launch_bounds__(256) void ls_score_f32_kernel(
   const int64_t t = i / n_pages_cols;
   const int p = (int)(i % n_pages_cols);
   int64_t a0, n_atoms;
-  if constexpr (SELECT) {
+  if constexpr (MODE == LS_SCORE_SELECT) {
     const int b = ls_find_segment(cu_q, batch, t);
     const int qp = (int)((t - cu_q[b]) / block_size);
     if (p < init_blocks || p > qp - local_blocks - 1) return;
     a0 = cu_a[b];
     n_atoms = (int64_t)cu_a[b + 1] - a0;
+  } else if constexpr (MODE == LS_SCORE_ALL) {
+    const int b = ls_find_segment(cu_q, batch, t);
+    a0 = cu_a[b];
+    n_atoms = (int64_t)cu_a[b + 1] - a0;
+    if ((int64_t)p > n_atoms / s) return;
   } else {
     if (p >= (full_seq_len + block_size - 1) / block_size) return;
     a0 = 0;
@@ -382,26 +399,14 @@ __global__ __launch_bounds__(256) void ls_score_f32_kernel(
   out[((int64_t)g * Nq + t) * out_stride + p] = best;
 }
 
+
 // ---------------------------------------------------------------------------
 // Top-k page selection.  One wave per (group, token) row.  The k'-th largest
 // order-preserving key T is found by bisection over the key bits, counting
-// with wave reductions over keys held in registers; pages above T and the
-// first (lowest-index) pages equal to T are emitted in ascending order
-// between the sink pages and the local pages.
+// with ballots over keys held in registers; pages above T and the first
+// (lowest-index) pages equal to T are emitted in ascending order between the
+// sink pages and the local pages.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t ls_order_key16(uint16_t b) {
-  return (b & 0x8000u) ? (~(uint32_t)b & 0xffffu) : ((uint32_t)b | 0x8000u);
-}
-__device__ __forceinline__ uint32_t ls_order_key32(uint32_t u) {
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Number of set bits of `mask` in the lanes below this one.
-__device__ __forceinline__ int ls_lanes_below(uint64_t mask) {
-  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-}
-
 // Top-kk of one row's cn candidate scores (columns base .. base + cn - 1 of
 // P), held as order-preserving keys in NS register slots of 64 lanes.  Loads
 // are issued together (addresses clamped into the row), then converted; keys
@@ -535,6 +540,26 @@ WsLayout ws_layout(int64_t total_q, int64_t total_atoms, int batch, int H, int G
   return L;
 }
 
+// The NOSA selection adds the per-sequence CIS page offsets and the CIS page
+// scores cpg[g][*] (at most total_atoms / 4 + batch pages per group).
+struct NosaWsLayout {
+  WsLayout L;
+  size_t pg, cpg, total;
+  int64_t cpg_stride;
+};
+
+NosaWsLayout nosa_ws_layout(int64_t total_q, int64_t total_atoms, int batch, int H, int G, int D,
+                            int F, int out_len, int eb) {
+  NosaWsLayout N;
+  N.L = ws_layout(total_q, total_atoms, batch, H, G, D, F, out_len, eb);
+  size_t off = N.L.total;
+  N.pg = off; off += ls_align256((size_t)(batch + 1) * 4);
+  N.cpg_stride = (total_atoms / 4 + batch + 63) & ~(int64_t)63;
+  N.cpg = off; off += ls_align256((size_t)G * N.cpg_stride * 4);
+  N.total = off;
+  return N;
+}
+
 int check_dims(const char* who, int H, int G, int D, int R, int RD, int dtype) {
   LS_REQUIRE(H > 0 && G > 0 && D > 0 && R > 0 && RD > 0, LS_ERR_INVALID, "%s: bad sizes", who);
   LS_REQUIRE(H % G == 0, LS_ERR_INVALID, "%s: num_heads must be divisible by num_kv_heads", who);
@@ -612,7 +637,7 @@ int project(int dtype, const void* A, int64_t lda, int64_t gk, int64_t M, int K,
   return launch_proj16<LS_F16>(A, lda, gk, M, K, F, G, wt, out, s);
 }
 
-template <int DT, bool SELECT>
+template <int DT, int MODE>
 int launch_score16(int F, dim3 grid, hipStream_t s, const void* qt, int64_t Nq, const void* kt,
                    int64_t Na, const int32_t* cu_q, const int32_t* cu_a, const int32_t* blk,
                    int batch, int64_t n_launch, int init_blocks, int local_blocks,
@@ -623,7 +648,7 @@ int launch_score16(int F, dim3 grid, hipStream_t s, const void* qt, int64_t Nq, 
   switch (F / 32) {
 #define LS_SCORE_CASE(KSV)                                                                   \
   case KSV:                                                                                  \
-    hipLaunchKernelGGL((ls_score_mfma_kernel<DT, KSV, SELECT>), grid, dim3(256), 0, s, qp, Nq, \
+    hipLaunchKernelGGL((ls_score_mfma_kernel<DT, KSV, MODE>), grid, dim3(256), 0, s, qp, Nq, \
                        kp, Na, cu_q, cu_a, blk, batch, n_launch, init_blocks, local_blocks,    \
                        full_len, op, out_stride);                                            \
     break;
@@ -641,7 +666,7 @@ int launch_score16(int F, dim3 grid, hipStream_t s, const void* qt, int64_t Nq, 
   return ls_check_launch("ls_score_mfma_kernel");
 }
 
-template <bool SELECT>
+template <int MODE>
 int score(int dtype, int F, const void* qt, int64_t Nq, const void* kt, int64_t Na,
           const int32_t* cu_q, const int32_t* cu_a, const int32_t* blk, int batch,
           int64_t n_blk_launch, int init_blocks, int local_blocks, int block_size,
@@ -651,7 +676,7 @@ int score(int dtype, int F, const void* qt, int64_t Nq, const void* kt, int64_t 
   if (dtype == LS_F32) {
     const int64_t n = Nq * n_page_cols;
     const dim3 grid((unsigned)((n + 255) / 256), G);
-    hipLaunchKernelGGL(ls_score_f32_kernel<SELECT>, grid, dim3(256), 0, s, (const float*)qt, Nq,
+    hipLaunchKernelGGL(ls_score_f32_kernel<MODE>, grid, dim3(256), 0, s, (const float*)qt, Nq,
                        (const float*)kt, Na, F, cu_q, cu_a, batch, init_blocks, local_blocks,
                        block_size, block_size / kernel_stride, full_len, n_page_cols,
                        (float*)out, out_stride);
@@ -660,12 +685,12 @@ int score(int dtype, int F, const void* qt, int64_t Nq, const void* kt, int64_t 
   LS_REQUIRE(block_size == 64 && kernel_stride == 16, LS_ERR_UNSUPPORTED,
              "score: the 16-bit path supports block_size 64 with kernel_stride 16 "
              "(got %d/%d)", block_size, kernel_stride);
-  const dim3 grid(SELECT ? (unsigned)n_blk_launch : (unsigned)((Nq + 63) / 64), G);
+  const dim3 grid(MODE != LS_SCORE_FULL ? (unsigned)n_blk_launch : (unsigned)((Nq + 63) / 64), G);
   if (dtype == LS_BF16)
-    return launch_score16<LS_BF16, SELECT>(F, grid, s, qt, Nq, kt, Na, cu_q, cu_a, blk, batch,
+    return launch_score16<LS_BF16, MODE>(F, grid, s, qt, Nq, kt, Na, cu_q, cu_a, blk, batch,
                                            n_blk_launch, init_blocks, local_blocks, full_len,
                                            out, out_stride);
-  return launch_score16<LS_F16, SELECT>(F, grid, s, qt, Nq, kt, Na, cu_q, cu_a, blk, batch,
+  return launch_score16<LS_F16, MODE>(F, grid, s, qt, Nq, kt, Na, cu_q, cu_a, blk, batch,
                                         n_blk_launch, init_blocks, local_blocks, full_len, out,
                                         out_stride);
 }
@@ -826,7 +851,7 @@ extern "C" int ls_score_pages(const void* query, int64_t q_row_stride, int64_t n
                     ws + L.kt, s)))
     return rc;
   const int64_t n_pages = (seq_len + block_size - 1) / block_size;
-  return score<false>(dtype, F, ws + L.qt, n_queries, ws + L.kt, n_atoms, nullptr, nullptr,
+  return score<LS_SCORE_FULL>(dtype, F, ws + L.qt, n_queries, ws + L.kt, n_atoms, nullptr, nullptr,
                       nullptr, 0, 0, 0, 0, block_size, kernel_stride, seq_len, n_pages, out,
                       n_pages, G, s);
 }
@@ -885,7 +910,7 @@ extern "C" int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t to
   if ((rc = ls_check_launch("ls_select_plan_kernel"))) return rc;
   const int64_t n_blk_launch = (total_q + block_size - 1) / block_size + batch;
   if (total_atoms > 0 &&
-      (rc = score<true>(dtype, F, ws + L.qt, total_q, ws + L.kt, total_atoms, cu_seqlens_q,
+      (rc = score<LS_SCORE_SELECT>(dtype, F, ws + L.qt, total_q, ws + L.kt, total_atoms, cu_seqlens_q,
                         cu_seqlens_kc, blk, batch, n_blk_launch, init_blocks, local_blocks,
                         block_size, kernel_stride, 0, max_pages, ws + L.p, L.p_stride, G, s)))
     return rc;
@@ -897,4 +922,92 @@ extern "C" int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t to
   return launch_topk<false>(max_pages, grid, s, ws + L.p, L.p_stride, cu_seqlens_q,
                             cu_seqlens_kc, batch, total_q, G, take, init_blocks, local_blocks,
                             block_size, topk_idx);
+}
+
+extern "C" size_t ls_nosa_select_workspace_size(int64_t total_q, int64_t total_atoms,
+                                                int32_t batch, int32_t num_heads,
+                                                int32_t num_kv_heads, int32_t head_dim,
+                                                int32_t router_heads, int32_t router_dim,
+                                                int32_t max_pages, int32_t dtype) {
+  return nosa_ws_layout(total_q, total_atoms, batch, num_heads, num_kv_heads, head_dim,
+                        router_heads * router_dim, max_pages, (int)ls_dtype_bytes(dtype))
+      .total;
+}
+
+// NOSA page plans (prefill): qk page scores of every page with atoms, the
+// qk shortlist, CIS page scores and the CIS top-k with the reference's masks
+// (leanselect/models/nosa.py:1144-1307 on the LeanSelect branch, whose atom
+// scores come from the folded router, nosa.py:1822-1853).
+extern "C" int ls_nosa_select_prefill(
+    const void* q, int64_t q_row_stride, int64_t total_q, const void* kc, int64_t kc_row_stride,
+    int64_t total_atoms, const void* cis, int64_t cis_row_stride, int32_t cis_dtype,
+    const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kc, const int32_t* cu_seqlens_k,
+    int32_t batch, int32_t max_seqlen_q, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_dim, const float* head_mix, const float* kv_head_mix, const float* q_proj,
+    const float* k_proj, int32_t router_heads, int32_t router_dim, int32_t dtype, int32_t topk,
+    int32_t block_size, int32_t kernel_stride, int32_t init_blocks, int32_t local_blocks,
+    int32_t select_blocks, int32_t* topk_idx, int32_t take, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  int rc = check_dims("ls_nosa_select_prefill", num_heads, num_kv_heads, head_dim, router_heads,
+                      router_dim, dtype);
+  if (rc) return rc;
+  LS_REQUIRE(batch >= 0 && total_q >= 0 && total_atoms >= 0 && max_seqlen_q >= 0, LS_ERR_INVALID,
+             "ls_nosa_select_prefill: bad sizes");
+  LS_REQUIRE(block_size == 64 && kernel_stride == 16, LS_ERR_UNSUPPORTED,
+             "ls_nosa_select_prefill: block_size 64 with kernel_stride 16 only (got %d/%d)",
+             block_size, kernel_stride);
+  LS_REQUIRE(cis_dtype == LS_F32 || cis_dtype == LS_BF16 || cis_dtype == LS_F16, LS_ERR_INVALID,
+             "ls_nosa_select_prefill: unknown CIS dtype %d", cis_dtype);
+  LS_REQUIRE(init_blocks >= 0 && local_blocks >= 0 && select_blocks >= 0 && topk >= 0,
+             LS_ERR_INVALID, "ls_nosa_select_prefill: block counts and topk must be >= 0");
+  const int out_len = (max_seqlen_q + block_size - 1) / block_size;
+  const int want = topk < out_len ? topk : out_len;
+  LS_REQUIRE(take == want, LS_ERR_INVALID,
+             "ls_nosa_select_prefill: take must be min(topk, ceil(max_seqlen_q / 64)) = %d", want);
+  if (total_q == 0 || batch == 0 || take == 0) return LS_OK;
+  LS_REQUIRE(q && kc && cis && cu_seqlens_q && cu_seqlens_kc && cu_seqlens_k && topk_idx,
+             LS_ERR_INVALID, "ls_nosa_select_prefill: null pointer");
+  const int qk_sel_raw = init_blocks + local_blocks + select_blocks;
+  const int qk_select = qk_sel_raw < out_len ? qk_sel_raw : out_len;
+  const int eb = (int)ls_dtype_bytes(dtype);
+  const int F = router_heads * router_dim, G = num_kv_heads, gs = num_heads / num_kv_heads;
+  const NosaWsLayout N = nosa_ws_layout(total_q, total_atoms, batch, num_heads, G, head_dim, F,
+                                        out_len, eb);
+  const WsLayout& L = N.L;
+  LS_REQUIRE(workspace && workspace_bytes >= N.total, LS_ERR_WORKSPACE,
+             "ls_nosa_select_prefill: workspace needs %zu bytes", N.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  int32_t* blk = (int32_t*)(ws + L.blk);
+  if ((rc = fuse_t(dtype, head_mix, q_proj, G, gs, router_heads, head_dim, router_dim,
+                   ws + L.wq, s)))
+    return rc;
+  if ((rc = fuse_t(dtype, kv_head_mix, k_proj, G, 1, router_heads, head_dim, router_dim,
+                   ws + L.wk, s)))
+    return rc;
+  if ((rc = project(dtype, q, q_row_stride, (int64_t)gs * head_dim, total_q, gs * head_dim, F,
+                    G, ws + L.wq, ws + L.qt, s)))
+    return rc;
+  if (total_atoms > 0 &&
+      (rc = project(dtype, kc, kc_row_stride, head_dim, total_atoms, head_dim, F, G, ws + L.wk,
+                    ws + L.kt, s)))
+    return rc;
+  hipLaunchKernelGGL(ls_select_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens_q, batch,
+                     block_size, blk);
+  if ((rc = ls_check_launch("ls_select_plan_kernel"))) return rc;
+  const int64_t n_blk_launch = (total_q + block_size - 1) / block_size + batch;
+  if (total_atoms > 0 &&
+      (rc = score<LS_SCORE_ALL>(dtype, F, ws + L.qt, total_q, ws + L.kt, total_atoms,
+                                cu_seqlens_q, cu_seqlens_kc, blk, batch, n_blk_launch,
+                                init_blocks, local_blocks, block_size, kernel_stride, out_len,
+                                out_len, ws + L.p, L.p_stride, G, s)))
+    return rc;
+  int32_t* pg_off = (int32_t*)(ws + N.pg);
+  float* cpg = (float*)(ws + N.cpg);
+  if ((rc = ls_nosa_cis_pages_launch(cis, cis_row_stride, cis_dtype, cu_seqlens_k, cu_seqlens_kc,
+                                     batch, total_atoms, G, pg_off, cpg, N.cpg_stride, s)))
+    return rc;
+  return ls_nosa_topk_launch(dtype, out_len, ws + L.p, L.p_stride, cpg, N.cpg_stride, pg_off,
+                             cu_seqlens_q, cu_seqlens_kc, batch, total_q, G, max_seqlen_q,
+                             init_blocks, local_blocks, qk_select, take, block_size, topk_idx, s);
 }

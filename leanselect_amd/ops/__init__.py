@@ -2,6 +2,8 @@
 from .attention import infllmv2_attn_varlen_func, sparse_attention
 from .compress import CompressK, compress_k
 from .select import leanselect_prefill_topk_idx, select_take
+from .cis_pooling import nosa_mean_pooling
+from .nosa import max_pooling_1d_varlen, nosa_prefill_topk_idx, nosa_sparse_attention
 from . import profiling
 
 __all__ = [
@@ -11,5 +13,9 @@ __all__ = [
     "select_take",
     "infllmv2_attn_varlen_func",
     "sparse_attention",
+    "nosa_mean_pooling",
+    "max_pooling_1d_varlen",
+    "nosa_prefill_topk_idx",
+    "nosa_sparse_attention",
     "profiling",
 ]

@@ -1,4 +1,4 @@
-"""Block-sparse prefill attention on the GPU (a10).
+"""Block-sparse prefill attention on the GPU.
 
 ``infllmv2_attn_varlen_func`` keeps the call surface the reference's model files
 use (leanselect/models/minicpm.py:3229-3243; nosa.py:2220-2251; wrapper contract

@@ -1,4 +1,4 @@
-"""Prefill page selection on the GPU (a2-a9).
+"""Prefill page selection on the GPU.
 
 Mirrors the LeanSelect branch of
 ``MiniCPMInfLLMv2Attention._lightweight_compressed_attention``

@@ -5,6 +5,11 @@ Follows the LeanSelect prefill branch of ``_sparse_attention_forward``
 (``compress_k``), select pages per KV group and token
 (``_lightweight_compressed_attention``), then block-sparse attention over the
 selected pages (``sparse_forward``).  Inputs are already unpadded/packed.
+
+``nosa_sparse_prefill`` is the LeanSelect branch of the NOSA layer's
+``sparse_forward`` (leanselect/models/nosa.py:1980-2255): the same
+compression, the two-stage qk/CIS selection (``compressed_attention``) and the
+CIS-biased attention.
 """
 from __future__ import annotations
 
@@ -13,9 +18,10 @@ import torch
 from .ops.attention import sparse_attention
 from .ops.compress import compress_k
 from .ops.profiling import range_pop, range_push
+from .ops.nosa import nosa_prefill_topk_idx, nosa_sparse_attention
 from .ops.select import leanselect_prefill_topk_idx
 
-__all__ = ["leanselect_sparse_prefill"]
+__all__ = ["leanselect_sparse_prefill", "nosa_sparse_prefill"]
 
 
 def leanselect_sparse_prefill(
@@ -54,5 +60,50 @@ def leanselect_sparse_prefill(
     range_push("stage 2")
     out = sparse_attention(q, k, v, cu_seqlens, cu_seqlens, max_len, max_len, ids,
                            causal=True, block_size=block_size)
+    range_pop()
+    return (out, ids) if return_topk_idx else out
+
+
+def nosa_sparse_prefill(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cis: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    selector,
+    *,
+    topk: int = 96,
+    init_blocks: int = 1,
+    local_blocks: int = 16,
+    select_blocks: int = 24,
+    block_size: int = 64,
+    kernel_size: int = 32,
+    kernel_stride: int = 16,
+    q_select: torch.Tensor | None = None,
+    cu_seqlens_host: list[int] | None = None,
+    return_topk_idx: bool = False,
+):
+    """``(out [total, H, D], topk_idx [G, total, take])`` of a NOSA layer.
+
+    ``cis [total, G]`` are the per-token eviction scores; ``q_select`` the
+    queries the selection sees (the reference passes the pre-RoPE queries when
+    it has them), ``q`` by default.
+    """
+    host = cu_seqlens_host if cu_seqlens_host is not None else cu_seqlens.tolist()
+    max_len = max(host[i + 1] - host[i] for i in range(len(host) - 1))
+    range_push("compress")
+    kc, cu_c = compress_k(k, cu_seqlens, kernel_size=kernel_size, kernel_stride=kernel_stride,
+                          cu_seqlens_host=host)
+    range_pop()
+    range_push("stage 1")
+    ids = nosa_prefill_topk_idx(
+        q if q_select is None else q_select, kc, cis, cu_seqlens, cu_c, cu_seqlens, selector,
+        topk=topk, init_blocks=init_blocks, local_blocks=local_blocks,
+        select_blocks=select_blocks, block_size=block_size, kernel_stride=kernel_stride,
+        max_seqlen_q=max_len, cu_seqlens_q_host=host)
+    range_pop()
+    range_push("stage 2")
+    out = nosa_sparse_attention(q, k, v, cis, cu_seqlens, cu_seqlens, max_len, max_len, ids,
+                                block_size=block_size)
     range_pop()
     return (out, ids) if return_topk_idx else out

@@ -51,7 +51,7 @@ def _round(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 
 
 # ----------------------------------------------------------------------------
-# a1: compressed keys
+# Compressed keys
 # ----------------------------------------------------------------------------
 def calc_chunks_with_stride(
     cu_seqlens: Sequence[int], kernel_size: int = 32, kernel_stride: int = 16
@@ -126,7 +126,7 @@ def compress_keys_mean(
 
 
 # ----------------------------------------------------------------------------
-# a2-a5: folded router weights, projections and atom scores
+# Folded router weights, projections and atom scores
 # ----------------------------------------------------------------------------
 def fused_weights(
     head_mix: torch.Tensor,
@@ -183,7 +183,7 @@ def atom_scores(q_tilde: torch.Tensor, k_tilde: torch.Tensor) -> torch.Tensor:
 
 
 # ----------------------------------------------------------------------------
-# a6, a7: page pooling and forced pages
+# Page pooling and forced pages
 # ----------------------------------------------------------------------------
 def pool_atoms_to_pages(
     atom_scores_: torch.Tensor,
@@ -243,7 +243,7 @@ def leanselect_take(cu_seqlens_q, topk: int, block_size: int = 64) -> int:
 
 
 # ----------------------------------------------------------------------------
-# a8, a9: the LeanSelect prefill selection driver
+# The LeanSelect prefill selection driver
 # ----------------------------------------------------------------------------
 def _stable_topk_desc(scores: torch.Tensor, k: int) -> torch.Tensor:
     """Indices of the ``k`` largest entries, ties to the lower index.
@@ -361,7 +361,7 @@ def select_prefill(
 
 
 # ----------------------------------------------------------------------------
-# a10: block-sparse causal attention over the selected pages
+# Block-sparse causal attention over the selected pages
 # ----------------------------------------------------------------------------
 def attention_keys_for_row(
     row: int,

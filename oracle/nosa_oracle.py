@@ -43,6 +43,8 @@ __all__ = [
     "nosa_atom_scores",
     "nosa_q_idx",
     "nosa_select_prefill",
+    "nosa_two_stage",
+    "nosa_pool_rows",
     "nosa_attention",
 ]
 
@@ -218,10 +220,22 @@ def nosa_select_prefill(
         block_cis[:, i] = pc.masked_fill(forced[None], float("inf"))
     q_idx_all = nosa_q_idx(cq, max_seqlen_q, block_size)
     q_idx = q_idx_all[torch.tensor(row_list, dtype=torch.long)] if R else q_idx_all[:0]
+    return nosa_two_stage(block, block_cis, q_idx, topk=topk,
+                          qk_select=init_blocks + local_blocks + select_blocks,
+                          return_scores=return_scores)
+
+
+def nosa_two_stage(block: torch.Tensor, block_cis: torch.Tensor, q_idx: torch.Tensor, *,
+                   topk: int, qk_select: int, return_scores: bool = False):
+    """The selection tail of ``compressed_attention`` (``nosa.py:1288-1305``) on
+    pooled page scores ``[G, R, out_len]`` (forced pages already ``+inf``):
+    CIS pages after ``q_idx`` ``-inf``; the ``min(qk_select, out_len)`` best qk
+    pages ``+inf`` in the CIS scores; the ``min(topk, out_len)`` best CIS pages
+    sorted, ids after ``q_idx`` replaced by ``-1``.  Ties go to the lower page."""
+    out_len = block.shape[-1]
     j_idx = torch.arange(out_len)[None, :]
     block_cis = block_cis.masked_fill((j_idx > q_idx[:, None])[None], float("-inf"))
-    qk_select = min(init_blocks + local_blocks + select_blocks, out_len)
-    short = _stable_topk_desc(block, qk_select)
+    short = _stable_topk_desc(block, min(int(qk_select), out_len))
     over = block_cis.clone()
     over.scatter_(2, short, float("inf"))
     k = min(int(topk), out_len)
@@ -231,6 +245,35 @@ def nosa_select_prefill(
     if return_scores:
         return idx, block, over
     return idx
+
+
+def nosa_pool_rows(page_qk: torch.Tensor, cis_means: torch.Tensor, cu_seqlens_q,
+                   cu_seqlens_kc, rows: Sequence[int], *, out_len: int, init_blocks: int,
+                   local_blocks: int, block_size: int = 64, kernel_stride: int = 16):
+    """Stage inputs of ``nosa_two_stage`` from given intermediate scores: qk page
+    scores ``page_qk [G, R, >= out_len]`` (pages without atoms ``-inf``) and
+    pooled CIS window means ``cis_means [G, total_q, M]`` (``nosa_mean_pooling``
+    layout), with the forced overlay of ``max_pooling_1d_varlen``.  Returns
+    ``(block, block_cis)`` ``[G, R, out_len]`` float64."""
+    cq = _as_list(cu_seqlens_q)
+    ckc = _as_list(cu_seqlens_kc)
+    s = block_size // kernel_stride
+    G = page_qk.shape[0]
+    R = len(rows)
+    block = torch.full((G, R, out_len), float("-inf"), dtype=torch.float64)
+    block_cis = torch.full((G, R, out_len), float("-inf"), dtype=torch.float64)
+    for i, r in enumerate(rows):
+        b = next(j for j in range(len(cq) - 1) if cq[j] <= r < cq[j + 1])
+        lk = ckc[b + 1] - ckc[b]
+        forced = _forced(torch.tensor([(r - cq[b]) // block_size]), out_len, init_blocks,
+                         local_blocks)[0]
+        n = min(out_len, page_qk.shape[-1])
+        pb = torch.full((G, out_len), float("-inf"), dtype=torch.float64)
+        pb[:, :n] = page_qk[:, i, :n].to(torch.float64)
+        pc = _pool_pages(cis_means[:, r].to(torch.float64), lk, out_len, s)
+        block[:, i] = pb.masked_fill(forced[None], float("inf"))
+        block_cis[:, i] = pc.masked_fill(forced[None], float("inf"))
+    return block, block_cis
 
 
 def nosa_attention(
@@ -246,11 +289,14 @@ def nosa_attention(
     block_size: int = 64,
     rows: Sequence[int] | None = None,
     ids_rows_aligned: bool = False,
-) -> torch.Tensor:
+    return_lse: bool = False,
+):
     """NOSA output ``[R, H, D]``: ``attn(q, k, V*e^cis) / attn(q, k, e^cis)``
     (``nosa.py:2211-2255``), i.e. ``sum_j w_j v_j / sum_j w_j`` with
     ``w_j = exp(scale * q.k_j + cis_j)`` over the causal keys of the row's pages.
-    Computed in float64 from that closed form and rounded once."""
+    Computed in float64 from that closed form and rounded once.  With
+    ``return_lse`` also ``log sum_j w_j`` ``[H, R]`` (``+inf`` for rows without
+    keys)."""
     cq = _as_list(cu_seqlens_q)
     ck = _as_list(cu_seqlens_k)
     total_q, H, D = q.shape
@@ -259,6 +305,7 @@ def nosa_attention(
     scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
     row_list = list(range(total_q)) if rows is None else [int(r) for r in rows]
     out = torch.zeros((len(row_list), H, D), dtype=torch.float64)
+    lse = torch.full((H, len(row_list)), float("inf"), dtype=torch.float64)
     qd, kd, vd = (x.detach().to(torch.float64) for x in (q, k, v))
     cd = cis.detach().to(torch.float64)
     for i, r in enumerate(row_list):
@@ -268,6 +315,10 @@ def nosa_attention(
             if keys.numel() == 0:
                 continue
             s = (qd[r, g * gs : (g + 1) * gs] @ kd[keys, g].T) * scale + cd[keys, g][None, :]
-            w = torch.exp(s - s.amax(dim=-1, keepdim=True))
+            m = s.amax(dim=-1, keepdim=True)
+            w = torch.exp(s - m)
             out[i, g * gs : (g + 1) * gs] = (w @ vd[keys, g]) / w.sum(dim=-1, keepdim=True)
+            lse[g * gs : (g + 1) * gs, i] = (m[:, 0] + torch.log(w.sum(dim=-1)))
+    if return_lse:
+        return _round(out, q.dtype), lse
     return _round(out, q.dtype)

@@ -53,6 +53,60 @@ def test_invalid_arguments_fail_before_any_launch():
     assert rc == _hip.LS_ERR_INVALID and b"take" in lib.ls_last_error()
 
 
+def test_nosa_entry_points_validate_before_any_launch():
+    lib = _hip.lib()
+    B = _hip.LS_BF16
+    # take must be min(topk, ceil(max_seqlen_q / 64)) = 2 for 100 tokens.
+    rc = lib.ls_nosa_select_prefill(None, 0, 100, None, 0, 5, None, 0, B, None, None, None, 1,
+                                    100, 32, 2, 128, None, None, None, None, 4, 32, B, 96, 64, 16,
+                                    1, 16, 24, None, 3, None, 0, None)
+    assert rc == _hip.LS_ERR_INVALID and b"take" in lib.ls_last_error()
+    rc = lib.ls_nosa_select_prefill(None, 0, 100, None, 0, 5, None, 0, B, None, None, None, 1,
+                                    100, 32, 2, 128, None, None, None, None, 4, 32, B, 96, 32, 16,
+                                    1, 16, 24, None, 2, None, 0, None)
+    assert rc == _hip.LS_ERR_UNSUPPORTED and b"block_size" in lib.ls_last_error()
+    rc = lib.ls_nosa_select_prefill(None, 0, 100, None, 0, 5, None, 0, 7, None, None, None, 1,
+                                    100, 32, 2, 128, None, None, None, None, 4, 32, B, 96, 64, 16,
+                                    1, 16, 24, None, 2, None, 0, None)
+    assert rc == _hip.LS_ERR_INVALID and b"CIS dtype" in lib.ls_last_error()
+    rc = lib.ls_nosa_attn_varlen(None, 0, None, 0, None, 0, None, 0, B, None, None, 1, 10, 10,
+                                 10, 10, 32, 2, 128, B, None, 1, 64, -1.0, None, None, None, 0,
+                                 None)
+    assert rc == _hip.LS_ERR_INVALID and b"CIS" in lib.ls_last_error()
+    rc = lib.ls_nosa_attn_varlen(None, 0, None, 0, None, 0, None, 0, B, None, None, 1, 10, 10,
+                                 10, 10, 32, 2, 64, B, None, 1, 64, -1.0, None, None, None, 0,
+                                 None)
+    assert rc in (_hip.LS_ERR_INVALID, _hip.LS_ERR_UNSUPPORTED)
+    rc = lib.ls_cis_mean_pool(None, 1, 10, 2, None, 1, 100, 16, 16, B, None, 5, None)
+    assert rc == _hip.LS_ERR_UNSUPPORTED
+    rc = lib.ls_cis_mean_pool(None, 1, 10, 2, None, 1, 100, 32, 16, B, None, 6, None)
+    assert rc == _hip.LS_ERR_INVALID and b"columns" in lib.ls_last_error()
+    rc = lib.ls_page_maxpool_varlen(None, None, None, None, 1, 2, 10, 10, 1, 2, 1, 64, 16, 9,
+                                    None, None)
+    assert rc == _hip.LS_ERR_INVALID and b"dtype" in lib.ls_last_error()
+    rc = lib.ls_page_maxpool_varlen(None, None, None, None, 1, 2, 10, 10, 1, 2, 1, 64, 48, B,
+                                    None, None)
+    assert rc == _hip.LS_ERR_INVALID
+
+
+def test_nosa_workspace_and_cpu_refusal():
+    lib = _hip.lib()
+    a = lib.ls_select_workspace_size(8192, 511, 1, 32, 2, 128, 4, 32, 128, _hip.LS_BF16)
+    b = lib.ls_nosa_select_workspace_size(8192, 511, 1, 32, 2, 128, 4, 32, 128, _hip.LS_BF16)
+    # + CIS page offsets and CIS page scores (2 groups x >= 511 / 4 + 1 floats).
+    assert b >= a + 2 * (511 // 4 + 1) * 4
+    assert (lib.ls_nosa_attn_workspace_size(131072, 1, 2, 128, 131072, _hip.LS_BF16)
+            >= lib.ls_sparse_attn_workspace_size(131072, 1, 2, 128, 131072, _hip.LS_BF16)
+            + 2 * 131072 * 4)
+    from leanselect_amd.ops import max_pooling_1d_varlen, nosa_mean_pooling
+    cu = torch.tensor([0, 64], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU"):
+        nosa_mean_pooling(torch.randn(64, 2), cu, 64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        max_pooling_1d_varlen(torch.randn(2, 64, 3), cu, torch.tensor([0, 3], dtype=torch.int32),
+                              torch.zeros(1, dtype=torch.int32), 64, 3, 1, 1)
+
+
 def test_workspace_sizes_are_host_only_and_grow():
     lib = _hip.lib()
     a = lib.ls_select_workspace_size(4096, 255, 1, 32, 2, 128, 4, 32, 64, _hip.LS_BF16)

@@ -15,7 +15,7 @@ GOLDEN = Path(__file__).with_name("golden")
 
 
 # --------------------------------------------------------------------------
-# a6: page pooling
+# Page pooling
 # --------------------------------------------------------------------------
 def test_pool_matches_reference_known_answers():
     data = json.loads((GOLDEN / "pool_pages.json").read_text())
@@ -49,7 +49,7 @@ def test_pool_rejects_bad_geometry():
 
 
 # --------------------------------------------------------------------------
-# a2-a5: folded projections
+# Folded projections
 # --------------------------------------------------------------------------
 def _small_selector(seed=7, H=8, G=2, D=8, R=2, RD=4):
     torch.manual_seed(seed)
@@ -111,7 +111,7 @@ def test_bf16_rounding_order_is_one_rounding_per_stage():
 
 
 # --------------------------------------------------------------------------
-# a1: compressed keys
+# Compressed keys
 # --------------------------------------------------------------------------
 def test_compress_k_is_window_mean_per_sequence():
     lens = [100, 31, 32, 48, 0, 77]
@@ -142,7 +142,7 @@ def test_compress_keys_mean_short_sequence_is_whole_mean():
 
 
 # --------------------------------------------------------------------------
-# a7-a9: selection
+# Selection
 # --------------------------------------------------------------------------
 def _brute_select(q, kc, cu, cu_c, qf, kf, topk, init, local, dtype):
     """Per-token loops: rounded dots, 5-atom max, forcing, sort by (-score, page)."""
@@ -237,7 +237,7 @@ def test_packed_selection_equals_independent_sequences():
 
 
 # --------------------------------------------------------------------------
-# a10: sparse attention
+# Sparse attention
 # --------------------------------------------------------------------------
 def _dense_masked(q, k, v, mask, scale):
     H, G = q.shape[1], k.shape[1]
