@@ -9,6 +9,11 @@ Prints one JSON line (metric: ms per layer, lower is better) with a roofline
 object for the dominant kernel (block-sparse attention) measured with HIP
 events on the launch stream, per-stage timings, and the CPU oracle timed on a
 bounded row sample of the same workload on this host.
+
+``--variant nosa`` times the NOSA layer instead (budget 96 pages = 1 sink +
+16 local + 79 chosen, shortlist 41, CIS-biased attention) on the same shapes;
+its CPU baseline is not run (the oracle's broadcast CIS pooling alone would
+need ~17 GB at 128K).
 """
 from __future__ import annotations
 
@@ -25,7 +30,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 from leanselect_amd import workloads  # noqa: E402
-from leanselect_amd.ops import compress_k, leanselect_prefill_topk_idx, sparse_attention  # noqa: E402
+from leanselect_amd.ops import (compress_k, leanselect_prefill_topk_idx,  # noqa: E402
+                                nosa_prefill_topk_idx, nosa_sparse_attention, sparse_attention)
 
 WORKLOADS = {
     "minicpm41_8b_layer_128k": dict(seq_lens=(131072,)),
@@ -58,8 +64,9 @@ def attention_keys(ids: torch.Tensor, cu_host: list[int]) -> int:
     return int((keys * valid).sum())
 
 
-def selection_flops(case, D: int = 128, F: int = 128) -> float:
-    """q~ projection + k~ projection + the atom dots of the non-forced visible pages."""
+def selection_flops(case, D: int = 128, F: int = 128, all_pages: bool = False) -> float:
+    """q~ projection + k~ projection + the atom dots of the non-forced visible pages
+    (of every page with atoms when ``all_pages``: the NOSA shortlist ranks them all)."""
     H, G = case.q.shape[1], case.k.shape[1]
     N = case.cu_host[-1]
     total = 2.0 * N * G * (H // G) * D * F
@@ -68,6 +75,9 @@ def selection_flops(case, D: int = 128, F: int = 128) -> float:
         n = case.cu_host[b + 1] - case.cu_host[b]
         A = (n - 32) // 16 + 1 if n >= 32 else 0
         total += 2.0 * A * G * D * F
+        if all_pages:
+            atom_dots += n * A
+            continue
         for qb in range((n + 63) // 64):
             hi = min(4 * (qb - case.local_blocks) - 1, A - 1)  # last atom of page qb-local-1
             lo = max(4 * case.init_blocks - 1, 0)
@@ -140,6 +150,7 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="minicpm41_8b_layer_128k", choices=sorted(WORKLOADS))
+    ap.add_argument("--variant", default="leanselect", choices=("leanselect", "nosa"))
     ap.add_argument("--kernel-iters", type=int, default=5)
     ap.add_argument("--cpu-rows-per-seq", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -157,16 +168,34 @@ def main() -> None:
     torch.cuda.set_device(dev)
     wl = WORKLOADS[args.workload]
     print(f"[bench] generating {args.workload} ...", file=sys.stderr, flush=True)
-    case = workloads.hidden_space_layer(wl["seq_lens"], device=dev, seed=0)
+    nosa = args.variant == "nosa"
+    if nosa:  # NOSA budget: topk 80 + 16 local, select_blocks 24 (nosa.py:643-676)
+        case = workloads.hidden_space_layer(wl["seq_lens"], device=dev, seed=0, topk=96,
+                                            local_blocks=16, init_blocks=1)
+        g = torch.Generator(device="cpu").manual_seed(1)
+        cis = torch.randn(case.cu_host[-1], case.k.shape[1], generator=g).to(torch.bfloat16).to(dev)
+    else:
+        case = workloads.hidden_space_layer(wl["seq_lens"], device=dev, seed=0)
     cu, cu_host = case.cu_seqlens, case.cu_host
     max_len = case.max_seqlen
     kw = dict(topk=case.topk, init_blocks=case.init_blocks, local_blocks=case.local_blocks,
               cu_seqlens_q_host=cu_host)
 
+    def select(kc, cu_c):
+        if nosa:
+            return nosa_prefill_topk_idx(case.q, kc, cis, cu, cu_c, cu, case.selector,
+                                         select_blocks=24, **kw)
+        return leanselect_prefill_topk_idx(case.q, kc, cu, cu_c, case.selector, **kw)
+
+    def attend(ids):
+        if nosa:
+            return nosa_sparse_attention(case.q, case.k, case.v, cis, cu, cu, max_len, max_len, ids)
+        return sparse_attention(case.q, case.k, case.v, cu, cu, max_len, max_len, ids)
+
     def step():
         kc, cu_c = compress_k(case.k, cu, cu_seqlens_host=cu_host)
-        ids = leanselect_prefill_topk_idx(case.q, kc, cu, cu_c, case.selector, **kw)
-        return sparse_attention(case.q, case.k, case.v, cu, cu, max_len, max_len, ids), ids
+        ids = select(kc, cu_c)
+        return attend(ids), ids
 
     if args.traffic_probe:
         # A plain device copy of known size calibrates the byte counters; then
@@ -195,17 +224,17 @@ def main() -> None:
     kc, cu_c = compress_k(case.k, cu, cu_seqlens_host=cu_host)
     it = args.kernel_iters
     ms_compress = _event_ms(lambda: compress_k(case.k, cu, cu_seqlens_host=cu_host), it)
-    ms_select = _event_ms(lambda: leanselect_prefill_topk_idx(case.q, kc, cu, cu_c, case.selector, **kw), it)
-    ms_attn = _event_ms(lambda: sparse_attention(case.q, case.k, case.v, cu, cu, max_len, max_len, ids), it)
+    ms_select = _event_ms(lambda: select(kc, cu_c), it)
+    ms_attn = _event_ms(lambda: attend(ids), it)
 
     H, G, D = case.q.shape[1], case.k.shape[1], case.q.shape[2]
     n_keys = attention_keys(ids, cu_host)
     attn_flops = 4.0 * (H // G) * D * n_keys
-    sel_flops = selection_flops(case)
+    sel_flops = selection_flops(case, all_pages=nosa)
     attn_tflops = attn_flops / (ms_attn * 1e-3) / 1e12
     N = cu_host[-1]
     result = {
-        "metric": "selector+sparse-attn prefill ms/layer @128K",
+        "metric": ("NOSA " if nosa else "") + "selector+sparse-attn prefill ms/layer @128K",
         "value": round(ms_step, 3),
         "unit": "ms/layer",
         "n_gpus": 1,
@@ -223,18 +252,20 @@ def main() -> None:
             "heads_q": H, "heads_kv": G, "head_dim": D, "page": 64,
             "budget_pages": case.topk, "sink_pages": case.init_blocks,
             "local_blocks": case.local_blocks, "router": "4x32",
+            **({"variant": "nosa", "select_blocks": 24, "cis": "bf16 N(0,1)"} if nosa else {}),
             "parallelism": "single-gpu",
         },
         "stages_ms": {"compress_k": round(ms_compress, 4), "select": round(ms_select, 4),
                       "sparse_attention": round(ms_attn, 4)},
         "roofline": {
-            "kernel": "ls_attn_tile_kernel (block-sparse attention; V staging and plan kernels excluded)",
+            "kernel": ("ls_attn_tile_kernel (block-sparse attention"
+                       + (", CIS key bias" if nosa else "") + "; timed with its V staging and plan kernels)"),
             "bound": "mfma",
             "achieved": round(attn_tflops, 2),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
-            "traffic": _traffic(args.workload),
+            "traffic": None if nosa else _traffic(args.workload),
             "algorithmic_flops": attn_flops,
             "avg_keys_per_row": round(n_keys / (G * N), 1),
         },
@@ -243,7 +274,7 @@ def main() -> None:
             "select_flops": sel_flops,
         },
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not nosa:
         threads = len(os.sched_getaffinity(0))
         print(f"[bench] CPU baseline on {threads} threads ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(case, args.cpu_rows_per_seq, threads)

@@ -260,7 +260,11 @@ __device__ __forceinline__ void ls_mark_topk(const uint32_t (&key)[NS], uint32_t
   }
 }
 
-template <int NS, bool KEY32>
+// Key widths: stage 1 uses 16-bit keys for 16-bit page scores (KEY32 off);
+// stage 2 uses the top 16 bits of the float32 keys when the CIS page scores
+// are bf16 values (CIS32 off: their low 16 bits are zero), so each bisection
+// runs over 16 bits instead of 32.
+template <int NS, bool KEY32, bool CIS32>
 __device__ __forceinline__ void ls_nosa_topk_row(
     const void* __restrict__ P, int64_t prow, const float* __restrict__ cpg_seq, int n_scored,
     int out_len, int off_bq, int q_idx, int init_blocks, int local_blocks, int qk_select,
@@ -269,7 +273,9 @@ __device__ __forceinline__ void ls_nosa_topk_row(
   // Every +inf (forced or shortlisted) and every -inf is one key, so ties among
   // them go to the lower page as in a stable sort.  Stage 1 keys come from the
   // page-score dtype (pinf1 / ninf1), stage 2 keys from float32.
-  const uint32_t pinf2 = ls_order_key32(0x7f800000u), ninf2 = ls_order_key32(0xff800000u);
+  constexpr int SH2 = CIS32 ? 0 : 16;
+  const uint32_t pinf2 = ls_order_key32(0x7f800000u) >> SH2;
+  const uint32_t ninf2 = ls_order_key32(0xff800000u) >> SH2;
   uint32_t key[NS];
   // Stage 1 keys.
 #pragma unroll
@@ -288,14 +294,14 @@ __device__ __forceinline__ void ls_nosa_topk_row(
     uint32_t k;
     if (p >= out_len) k = 0u;
     else if (p < init_blocks || (off_bq - local_blocks <= p && p <= off_bq)) k = pinf1;
-    else if (p < n_scored) k = KEY32 ? ls_order_key32(key[s]) : (ls_order_key16((uint16_t)key[s]) << 16);
+    else if (p < n_scored) k = KEY32 ? ls_order_key32(key[s]) : ls_order_key16((uint16_t)key[s]);
     else k = ninf1;
     key[s] = k;
   }
   uint32_t shortlist[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) shortlist[i] = 0u;
-  ls_mark_topk<NS>(key, ls_kth_key<NS, 32>(key, qk_select), qk_select, shortlist);
+  ls_mark_topk<NS>(key, ls_kth_key<NS, KEY32 ? 32 : 16>(key, qk_select), qk_select, shortlist);
   // Stage 2 keys.
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
@@ -308,13 +314,13 @@ __device__ __forceinline__ void ls_nosa_topk_row(
     else if (p > q_idx) k = ninf2;
     else if (p < init_blocks || (off_bq - local_blocks <= p && p <= off_bq)) k = pinf2;
     else if (p >= n_scored) k = ninf2;
-    else k = ls_order_key32(__builtin_bit_cast(uint32_t, cpg_seq[p]));
+    else k = ls_order_key32(__builtin_bit_cast(uint32_t, cpg_seq[p])) >> SH2;
     key[s] = k;
   }
   uint32_t chosen[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) chosen[i] = 0u;
-  ls_mark_topk<NS>(key, ls_kth_key<NS, 32>(key, take), take, chosen);
+  ls_mark_topk<NS>(key, ls_kth_key<NS, CIS32 ? 32 : 16>(key, take), take, chosen);
   // Emission: chosen pages <= q_idx in ascending order, then -1.
   int out_pos = 0;
 #pragma unroll
@@ -328,7 +334,7 @@ __device__ __forceinline__ void ls_nosa_topk_row(
   for (int i = out_pos + lane; i < take; i += 64) orow[i] = -1;
 }
 
-template <int KPL, bool KEY32>
+template <int KPL, bool KEY32, bool CIS32>
 __global__ __launch_bounds__(256) void ls_nosa_topk_kernel(
     const void* __restrict__ P, int64_t p_stride, const float* __restrict__ cpg, int64_t cpg_g_stride,
     const int32_t* __restrict__ pg_off, const int32_t* __restrict__ cu_q,
@@ -352,24 +358,24 @@ __global__ __launch_bounds__(256) void ls_nosa_topk_kernel(
   int32_t* orow = topk_idx + row * take;
   const int64_t prow = row * p_stride;
   const int n_slots = (out_len + 63) >> 6;
-  if (n_slots <= 1) return ls_nosa_topk_row<1, KEY32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 2) return ls_nosa_topk_row<2, KEY32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 4 || KPL <= 4) return ls_nosa_topk_row<(KPL < 4 ? KPL : 4), KEY32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 8 || KPL <= 8) return ls_nosa_topk_row<(KPL < 8 ? KPL : 8), KEY32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 16 || KPL <= 16) return ls_nosa_topk_row<(KPL < 16 ? KPL : 16), KEY32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 32 || KPL <= 32) return ls_nosa_topk_row<(KPL < 32 ? KPL : 32), KEY32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 64 || KPL <= 64) return ls_nosa_topk_row<(KPL < 64 ? KPL : 64), KEY32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  return ls_nosa_topk_row<KPL, KEY32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
+  if (n_slots <= 1) return ls_nosa_topk_row<1, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
+  if (n_slots <= 2) return ls_nosa_topk_row<2, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
+  if (n_slots <= 4 || KPL <= 4) return ls_nosa_topk_row<(KPL < 4 ? KPL : 4), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
+  if (n_slots <= 8 || KPL <= 8) return ls_nosa_topk_row<(KPL < 8 ? KPL : 8), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
+  if (n_slots <= 16 || KPL <= 16) return ls_nosa_topk_row<(KPL < 16 ? KPL : 16), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
+  if (n_slots <= 32 || KPL <= 32) return ls_nosa_topk_row<(KPL < 32 ? KPL : 32), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
+  if (n_slots <= 64 || KPL <= 64) return ls_nosa_topk_row<(KPL < 64 ? KPL : 64), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
+  return ls_nosa_topk_row<KPL, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
 }
 
-template <bool KEY32>
+template <bool KEY32, bool CIS32>
 static int launch_nosa_topk_k(int out_len, dim3 grid, hipStream_t s, const void* P, int64_t ps,
                               const float* cpg, int64_t cs, const int32_t* pg_off,
                               const int32_t* cu_q, const int32_t* cu_a, int batch, int64_t total_q,
                               int G, int max_q, int init, int local, int qk_select, int take,
                               int bs, uint32_t pinf1, uint32_t ninf1, int32_t* out) {
 #define LS_NOSA_TOPK(K)                                                                          \
-  hipLaunchKernelGGL((ls_nosa_topk_kernel<K, KEY32>), grid, dim3(256), 0, s, P, ps, cpg, cs,    \
+  hipLaunchKernelGGL((ls_nosa_topk_kernel<K, KEY32, CIS32>), grid, dim3(256), 0, s, P, ps, cpg, cs,    \
                      pg_off, cu_q, cu_a, batch, total_q, G, max_q, out_len, init, local,       \
                      qk_select, take, bs, pinf1, ninf1, out)
   if (out_len <= 256) LS_NOSA_TOPK(4);
@@ -382,23 +388,25 @@ static int launch_nosa_topk_k(int out_len, dim3 grid, hipStream_t s, const void*
   return ls_check_launch("ls_nosa_topk_kernel");
 }
 
-int ls_nosa_topk_launch(int p_dtype, int out_len, const void* P, int64_t p_stride, const float* cpg,
+int ls_nosa_topk_launch(int p_dtype, int cis_dtype, int out_len, const void* P, int64_t p_stride, const float* cpg,
                         int64_t cpg_g_stride, const int32_t* pg_off, const int32_t* cu_q,
                         const int32_t* cu_a, int batch, int64_t total_q, int G, int max_seqlen_q,
                         int init_blocks, int local_blocks, int qk_select, int take,
                         int block_size, int32_t* topk_idx, hipStream_t s) {
   if (total_q == 0 || G == 0 || take == 0) return LS_OK;
   const dim3 grid((unsigned)(((int64_t)G * total_q + 3) / 4));
-  if (p_dtype == LS_F32)
-    return launch_nosa_topk_k<true>(out_len, grid, s, P, p_stride, cpg, cpg_g_stride, pg_off, cu_q,
-                                    cu_a, batch, total_q, G, max_seqlen_q, init_blocks,
-                                    local_blocks, qk_select, take, block_size,
-                                    ls_order_key32(0x7f800000u), ls_order_key32(0xff800000u),
-                                    topk_idx);
-  const uint16_t pinf = p_dtype == LS_BF16 ? 0x7f80u : 0x7c00u;
-  const uint16_t ninf = p_dtype == LS_BF16 ? 0xff80u : 0xfc00u;
-  return launch_nosa_topk_k<false>(out_len, grid, s, P, p_stride, cpg, cpg_g_stride, pg_off, cu_q,
-                                   cu_a, batch, total_q, G, max_seqlen_q, init_blocks, local_blocks,
-                                   qk_select, take, block_size, ls_order_key16(pinf) << 16,
-                                   ls_order_key16(ninf) << 16, topk_idx);
+  const bool cis16 = cis_dtype == LS_BF16;
+#define LS_NOSA_TOPK_ARGS                                                                      \
+  out_len, grid, s, P, p_stride, cpg, cpg_g_stride, pg_off, cu_q, cu_a, batch, total_q, G,   \
+      max_seqlen_q, init_blocks, local_blocks, qk_select, take, block_size, pinf, ninf, topk_idx
+  if (p_dtype == LS_F32) {
+    const uint32_t pinf = ls_order_key32(0x7f800000u), ninf = ls_order_key32(0xff800000u);
+    return cis16 ? launch_nosa_topk_k<true, false>(LS_NOSA_TOPK_ARGS)
+                 : launch_nosa_topk_k<true, true>(LS_NOSA_TOPK_ARGS);
+  }
+  const uint32_t pinf = ls_order_key16(p_dtype == LS_BF16 ? 0x7f80u : 0x7c00u);
+  const uint32_t ninf = ls_order_key16(p_dtype == LS_BF16 ? 0xff80u : 0xfc00u);
+  return cis16 ? launch_nosa_topk_k<false, false>(LS_NOSA_TOPK_ARGS)
+               : launch_nosa_topk_k<false, true>(LS_NOSA_TOPK_ARGS);
+#undef LS_NOSA_TOPK_ARGS
 }

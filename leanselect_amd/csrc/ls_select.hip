@@ -1007,7 +1007,7 @@ extern "C" int ls_nosa_select_prefill(
   if ((rc = ls_nosa_cis_pages_launch(cis, cis_row_stride, cis_dtype, cu_seqlens_k, cu_seqlens_kc,
                                      batch, total_atoms, G, pg_off, cpg, N.cpg_stride, s)))
     return rc;
-  return ls_nosa_topk_launch(dtype, out_len, ws + L.p, L.p_stride, cpg, N.cpg_stride, pg_off,
+  return ls_nosa_topk_launch(dtype, cis_dtype, out_len, ws + L.p, L.p_stride, cpg, N.cpg_stride, pg_off,
                              cu_seqlens_q, cu_seqlens_kc, batch, total_q, G, max_seqlen_q,
                              init_blocks, local_blocks, qk_select, take, block_size, topk_idx, s);
 }

@@ -79,15 +79,13 @@ def nosa_sparse_prefill(
     block_size: int = 64,
     kernel_size: int = 32,
     kernel_stride: int = 16,
-    q_select: torch.Tensor | None = None,
     cu_seqlens_host: list[int] | None = None,
     return_topk_idx: bool = False,
 ):
     """``(out [total, H, D], topk_idx [G, total, take])`` of a NOSA layer.
 
-    ``cis [total, G]`` are the per-token eviction scores; ``q_select`` the
-    queries the selection sees (the reference passes the pre-RoPE queries when
-    it has them), ``q`` by default.
+    ``cis [total, G]`` are the per-token eviction scores.  The selection scores
+    the post-RoPE queries, as the LeanSelect branch does (nosa.py:2011-2019).
     """
     host = cu_seqlens_host if cu_seqlens_host is not None else cu_seqlens.tolist()
     max_len = max(host[i + 1] - host[i] for i in range(len(host) - 1))
@@ -97,7 +95,7 @@ def nosa_sparse_prefill(
     range_pop()
     range_push("stage 1")
     ids = nosa_prefill_topk_idx(
-        q if q_select is None else q_select, kc, cis, cu_seqlens, cu_c, cu_seqlens, selector,
+        q, kc, cis, cu_seqlens, cu_c, cu_seqlens, selector,
         topk=topk, init_blocks=init_blocks, local_blocks=local_blocks,
         select_blocks=select_blocks, block_size=block_size, kernel_stride=kernel_stride,
         max_seqlen_q=max_len, cu_seqlens_q_host=host)
