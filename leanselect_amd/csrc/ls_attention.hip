@@ -221,10 +221,12 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   __shared__ uint16_t s_union[LS_ATT_MAX_UNION];
   __shared__ int8_t s_uexp[LS_ATT_MAX_UNION];
   __shared__ uint32_t s_umask[LS_ATT_MAX_UNION];
+  __shared__ uint8_t s_uneed[LS_ATT_MAX_UNION];  // waves with a row on the page
   __shared__ int s_wsum[LS_ATT_WAVES];
   // Ring protocol: s_next = next union page to be claimed for copying;
   // s_ready[st] = union index + 1 of the page whose copy into stage st has
-  // landed; s_done[st] = waves finished with stage st, over all its pages.
+  // landed; s_done[st] = (union index << 8) | number of its waves done with it,
+  // for the page in stage st (tagged, so a stale count never matches).
   __shared__ uint32_t s_next, s_ready[LS_ATT_STAGES], s_done[LS_ATT_STAGES];
   __shared__ __align__(16) float s_bias[BIAS ? LS_ATT_STAGES * 64 : 4];
   static_assert(LS_ATT_TILE * LS_ATT_WORDS * 4 <= LS_ATT_STAGES * LS_ATT_STAGE_BYTES,
@@ -332,8 +334,12 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
 #pragma unroll
     for (int i = 0; i < LS_ATT_TILE; ++i) rows |= ((s_bits[i][tid] >> bit) & 1u) << i;
     const int dst = (int)(((uint32_t)pos * (uint32_t)stride) % (uint32_t)n_union);
+    int n_waves = 0;
+#pragma unroll
+    for (int i = 0; i < LS_ATT_WAVES; ++i) n_waves += ((rows >> (LS_ATT_TPW * i)) & ROWS_MASK) != 0u;
     s_uexp[dst] = (int8_t)vexp_seq[page];
     s_umask[dst] = rows;
+    s_uneed[dst] = (uint8_t)n_waves;
     s_union[dst] = (uint16_t)page;
     ++pos;
   }
@@ -365,6 +371,14 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   __syncthreads();  // union list, exponents and every wave's Q loads are complete;
                     // the bitmaps are dead, so the ring may be written
   LS_WAIT_VMCNT(0);
+  // This wave's pages: bit b of lane l is set when one of its rows selected
+  // union page 32 l + b (the union holds at most 64 x 32 pages).
+  static_assert(LS_ATT_MAX_UNION <= 64 * 32, "one need word per lane");
+  uint32_t wneed = 0u;
+  for (int b = 0; b < 32; ++b) {
+    const int u = 32 * lane + b;
+    if (u < n_union && ((s_umask[u] >> (LS_ATT_TPW * w)) & ROWS_MASK) != 0u) wneed |= 1u << b;
+  }
 
   // ---- staging ----
   // One wave copies a whole union page into its stage: K as 64 rows of 256 B
@@ -373,12 +387,13 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   // so the sixteen lanes of an MFMA operand read hit sixteen distinct bank
   // groups.  Each copy fills 1 KB of contiguous LDS (lane l -> byte 16 l).
   //
-  // Waves are not kept in lockstep.  A wave waits only for the page it is
-  // about to read; while it waits it does the copying: it claims the next
-  // unclaimed page (at most three ahead of itself) once every wave is done
-  // with that page's stage, copies it, waits for its own copy and marks the
-  // page ready.  Busy waves never hold an unmarked copy, so a waiting wave
-  // depends only on pages that are marked or being copied by a waiting wave.
+  // Waves are not kept in lockstep, and a wave visits only the pages its rows
+  // selected.  It waits only for the page it is about to read; while it waits
+  // it does the copying: it claims the next unclaimed page (at most three
+  // ahead of itself) once every wave with rows on the stage's previous page
+  // is done with it, copies it, waits for its own copy and marks the page
+  // ready.  Busy waves never hold an unmarked copy, so a waiting wave depends
+  // only on pages that are marked or being copied by a waiting wave.
   const uint16_t* kgrp = kg + (int64_t)g * D;
   const uint16_t* vgrp = vt + (int64_t)g * D * lpad + vbase;
   const float* cgrp = BIAS ? cb + (int64_t)g * lpad + vbase : nullptr;
@@ -433,17 +448,23 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     const int nx = __builtin_amdgcn_readfirstlane(
         (int)__hip_atomic_load(&s_next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
     if (nx >= n_union || nx > ui + LS_ATT_STAGES - 1) return;
-    const uint32_t gen = (uint32_t)nx / LS_ATT_STAGES;
-    if (gen > 0 && (uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
-                       &s_done[nx % LS_ATT_STAGES], __ATOMIC_ACQUIRE,
-                       __HIP_MEMORY_SCOPE_WORKGROUP)) < LS_ATT_WAVES * gen)
-      return;  // a wave may still read the stage's previous page
+    if (nx >= LS_ATT_STAGES) {
+      const int prev = nx - LS_ATT_STAGES;
+      const uint32_t want = ((uint32_t)prev << 8) | (uint32_t)s_uneed[prev];
+      if ((uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
+              &s_done[nx % LS_ATT_STAGES], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) != want)
+        return;  // a wave may still read the stage's previous page
+    }
     int won = 0;
     if (lane == 0) {
       uint32_t expect = (uint32_t)nx;
       won = __hip_atomic_compare_exchange_strong(&s_next, &expect, (uint32_t)nx + 1u,
                                                  __ATOMIC_ACQ_REL, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_WORKGROUP);
+      // The stage now belongs to page nx: its readers count from zero.
+      if (won)
+        __hip_atomic_store(&s_done[nx % LS_ATT_STAGES], (uint32_t)nx << 8, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     if (__builtin_amdgcn_readfirstlane(won)) {
       issue_page(nx);
@@ -580,7 +601,16 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     }
   };
 
-  for (int ui = 0; ui < n_union; ++ui) {
+  // Next page of this wave: the lowest set need bit above `after` (n_union if none).
+  auto next_page = [&](int after) -> int {
+    const int from = after + 1, fl = from >> 5;
+    const uint32_t word = lane < fl ? 0u : (lane == fl ? wneed & (0xffffffffu << (from & 31)) : wneed);
+    const uint64_t lanes = __ballot(word != 0u);
+    if (lanes == 0ull) return n_union;
+    const int L = (int)__builtin_ctzll(lanes);
+    return 32 * L + (int)__builtin_ctz((uint32_t)__builtin_amdgcn_readlane((int)word, L));
+  };
+  for (int ui = next_page(-1); ui < n_union; ui = next_page(ui)) {
     if (!is_ready(ui)) {
       // Bounded wait (the protocol cannot deadlock; the bound only guarantees
       // that a wave always finishes).
@@ -594,7 +624,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
 
     const int page = s_union[ui];
     const uint32_t sel = __builtin_amdgcn_readfirstlane((s_umask[ui] >> (LS_ATT_TPW * w)) & ROWS_MASK);
-    if (sel) compute_page(ui, page, sel);
+    compute_page(ui, page, sel);
     // Done with the stage (the release orders this wave's reads of it first).
     if (lane == 0)
       __hip_atomic_fetch_add(&s_done[ui % LS_ATT_STAGES], 1u, __ATOMIC_RELEASE,
