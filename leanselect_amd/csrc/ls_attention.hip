@@ -52,11 +52,15 @@ __device__ __forceinline__ int ls_wave_excl_scan(int v, int lane, int* total) {
 
 // pg_off[b] = sum_{b' < b} ceil(len_k(b') / 64): page-aligned start of each
 // sequence in the transposed V copy (in pages); tile_off[b] = sum_{b' < b}
-// ceil(len_q(b') / tile): first row tile of each sequence.
+// ceil(len_q(b') / tile): first row tile of each sequence; tok[i] = i for
+// i < n_tok (the ready tokens the tile kernel's copies deliver).
 __global__ void ls_attn_plan_kernel(const int32_t* __restrict__ cu_q,
                                     const int32_t* __restrict__ cu_k, int batch, int tile,
-                                    int32_t* __restrict__ pg_off, int32_t* __restrict__ tile_off) {
-  if (LS_TID != 0 || LS_BID_X != 0) return;
+                                    int32_t* __restrict__ pg_off, int32_t* __restrict__ tile_off,
+                                    int32_t* __restrict__ tok, int n_tok) {
+  if (LS_BID_X != 0) return;
+  for (int i = LS_TID; i < n_tok; i += 64) tok[i] = i;
+  if (LS_TID != 0) return;
   int32_t acc = 0, acc_t = 0;
   pg_off[0] = 0;
   tile_off[0] = 0;
@@ -180,9 +184,23 @@ __device__ __forceinline__ void ls_dma16(const void* sbase, uint32_t voff, uint3
                       (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(voff), "s"(sa), "s"(lds_off)
+               : "v"(voff), "s"(sa), "s"((uint32_t)__builtin_amdgcn_readfirstlane(lds_off))
                : "memory", "m0");
 }
+
+// One 4-byte global->LDS load per active lane (lane l lands at lds_off + 4 l).
+__device__ __forceinline__ void ls_dma4(const void* sbase, uint32_t voff, uint32_t lds_off) {
+  const uint64_t a = (uint64_t)(uintptr_t)sbase;
+  const uint64_t sa = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
+                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :
+               : "v"(voff), "s"(sa), "s"((uint32_t)__builtin_amdgcn_readfirstlane(lds_off))
+               : "memory", "m0");
+}
+
+// lgkmcnt(0) with the other counters left alone (gfx9 encoding).
+#define LS_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(0xf | (0x7 << 4) | (0x3 << 14))
 
 // Two float32 -> one packed fp16 pair (round to nearest even).
 __device__ __forceinline__ uint32_t ls_pack_f16x2(float a, float b) {
@@ -207,7 +225,8 @@ template <int DT, bool BIAS>
 __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_tile_kernel(
     const uint16_t* __restrict__ qg, int64_t q_rs, const uint16_t* __restrict__ kg,
     int64_t k_rs, const uint16_t* __restrict__ vt, int64_t lpad,
-    const int32_t* __restrict__ vexp, const float* __restrict__ cb, int64_t n_pages_ws,
+    const int32_t* __restrict__ vexp, const float* __restrict__ cb,
+    const int32_t* __restrict__ tok, int64_t n_pages_ws,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
     const int32_t* __restrict__ pg_off, const int32_t* __restrict__ tile_off, int batch,
     int64_t total_q, int G, int gs, const int32_t* __restrict__ topk_idx, int take,
@@ -225,8 +244,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   __shared__ int s_wsum[LS_ATT_WAVES];
   // Ring protocol: s_next = next union page to be claimed for copying;
   // s_ready[st] = union index + 1 of the page whose copy into stage st has
-  // landed; s_done[st] = (union index << 8) | number of its waves done with it,
-  // for the page in stage st (tagged, so a stale count never matches).
+  // landed; s_done[st] = (union index << 8) | number of its waves done with
+  // it, for the page in stage st (tagged, so a stale count never matches).
   __shared__ uint32_t s_next, s_ready[LS_ATT_STAGES], s_done[LS_ATT_STAGES];
   __shared__ __align__(16) float s_bias[BIAS ? LS_ATT_STAGES * 64 : 4];
   static_assert(LS_ATT_TILE * LS_ATT_WORDS * 4 <= LS_ATT_STAGES * LS_ATT_STAGE_BYTES,
@@ -276,7 +295,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     s_ready[tid] = 0u;
     s_done[tid] = 0u;
   }
-  if (tid == 0) s_next = 0u;
+  if (tid == 0) s_next = LS_ATT_STAGES;  // pages 0..3 are copied at the start
   __syncthreads();
   if (last_page >= 0) {
     const int32_t* ids = topk_idx + ((int64_t)g * total_q + t0) * take;
@@ -388,16 +407,20 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   // groups.  Each copy fills 1 KB of contiguous LDS (lane l -> byte 16 l).
   //
   // Waves are not kept in lockstep, and a wave visits only the pages its rows
-  // selected.  It waits only for the page it is about to read; while it waits
-  // it does the copying: it claims the next unclaimed page (at most three
-  // ahead of itself) once every wave with rows on the stage's previous page
-  // is done with it, copies it, waits for its own copy and marks the page
-  // ready.  Busy waves never hold an unmarked copy, so a waiting wave depends
-  // only on pages that are marked or being copied by a waiting wave.
+  // selected, waiting only for the page it is about to read.  Union page u
+  // goes to stage u % 4.  The copies of pages 0..3 are issued at the start.
+  // A waiting wave claims the next unclaimed page (at most three ahead of the
+  // page it waits for) once every wave with rows on the stage's previous page
+  // is done with it, issues its copy and goes back to waiting without
+  // waiting for the copy: the copy's final load brings the page's token
+  // (union index + 1) from global memory into s_ready[stage], and a wave's
+  // loads land in issue order, so the token lands after the page's K, V^T and
+  // bias.  Computing waves never copy (the last wave on a page is often the
+  // slowest one).  A page's copy depends only on earlier pages being
+  // finished, so every wait ends.
   const uint16_t* kgrp = kg + (int64_t)g * D;
   const uint16_t* vgrp = vt + (int64_t)g * D * lpad + vbase;
   const float* cgrp = BIAS ? cb + (int64_t)g * lpad + vbase : nullptr;
-  ls_u32x4 pending_cb = {0u, 0u, 0u, 0u};  // bias of the page being copied (lanes 0..15)
   const uint32_t ring_off = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(ls_lds_void*)s_ring);
   const int64_t k_rs_bytes = 2 * k_rs;
@@ -438,50 +461,46 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     const uint16_t* vpage = vgrp + 64LL * page;
 #pragma unroll
     for (int i = 0; i < 16; ++i) ls_dma16(vpage + 8LL * i * lpad, v_lane[i & 1], vb + i * 1024);
-    // The page's 64 biases go through registers (stored to LDS once landed).
+    // The page's 64 biases (lanes 0..15, 16 bytes each).
     if constexpr (BIAS)
-      if (lane < 16) pending_cb = *reinterpret_cast<const ls_u32x4*>(cgrp + 64LL * page + 4 * lane);
+      if (lane < 16)
+        ls_dma16(cgrp + 64LL * page, 16u * (uint32_t)lane,
+                 (uint32_t)(uintptr_t)(ls_lds_void*)s_bias + (ui_copy % LS_ATT_STAGES) * 256u);
+    // Last: the ready token ui_copy + 1 into s_ready[stage] (lane 0 only).
+    if (lane == 0)
+      ls_dma4(tok + ui_copy + 1, 0u,
+              (uint32_t)(uintptr_t)(ls_lds_void*)&s_ready[ui_copy % LS_ATT_STAGES]);
   };
-  int pending = -1;  // union index this wave copied and has not marked ready
+  // Hands stage u % 4 to page u (its waves count from zero) and copies it.
+  auto issue_copy = [&](int u) {
+    if (lane == 0)
+      __hip_atomic_store(&s_done[u % LS_ATT_STAGES], (uint32_t)u << 8, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_WORKGROUP);
+    LS_WAIT_LGKMCNT0();  // the count is reset before the token can land
+    issue_page(u);
+  };
+  // A waiting wave at page ui claims and copies page s_next when its stage is free.
   auto try_claim = [&](int ui) {
-    if (pending >= 0) return;
     const int nx = __builtin_amdgcn_readfirstlane(
         (int)__hip_atomic_load(&s_next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-    if (nx >= n_union || nx > ui + LS_ATT_STAGES - 1) return;
-    if (nx >= LS_ATT_STAGES) {
-      const int prev = nx - LS_ATT_STAGES;
-      const uint32_t want = ((uint32_t)prev << 8) | (uint32_t)s_uneed[prev];
-      if ((uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
-              &s_done[nx % LS_ATT_STAGES], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) != want)
-        return;  // a wave may still read the stage's previous page
-    }
+    if (nx >= n_union || nx > ui + LS_ATT_STAGES - 1) return false;
+    const int prev = nx - LS_ATT_STAGES;  // >= 0: pages 0..3 are copied at the start
+    const uint32_t want = ((uint32_t)prev << 8) | (uint32_t)s_uneed[prev];
+    if ((uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
+            &s_done[nx % LS_ATT_STAGES], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) != want)
+      return false;  // a wave may still read the stage's previous page
     int won = 0;
     if (lane == 0) {
       uint32_t expect = (uint32_t)nx;
       won = __hip_atomic_compare_exchange_strong(&s_next, &expect, (uint32_t)nx + 1u,
                                                  __ATOMIC_ACQ_REL, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_WORKGROUP);
-      // The stage now belongs to page nx: its readers count from zero.
-      if (won)
-        __hip_atomic_store(&s_done[nx % LS_ATT_STAGES], (uint32_t)nx << 8, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    if (__builtin_amdgcn_readfirstlane(won)) {
-      issue_page(nx);
-      pending = nx;
-    }
+    if (!__builtin_amdgcn_readfirstlane(won)) return false;
+    issue_copy(nx);
+    return true;
   };
-  auto mark_ready = [&]() {
-    if (pending < 0) return;
-    LS_WAIT_VMCNT(0);  // this wave's copies are its only outstanding loads
-    if constexpr (BIAS)
-      if (lane < 16)
-        *reinterpret_cast<ls_u32x4*>(s_bias + (pending % LS_ATT_STAGES) * 64 + 4 * lane) = pending_cb;
-    if (lane == 0)
-      __hip_atomic_store(&s_ready[pending % LS_ATT_STAGES], (uint32_t)pending + 1u,
-                         __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    pending = -1;
-  };
+  if (w < LS_ATT_STAGES && w < n_union) issue_copy(w);
   auto is_ready = [&](int ui) {
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
                &s_ready[ui % LS_ATT_STAGES], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) ==
@@ -615,10 +634,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       // Bounded wait (the protocol cannot deadlock; the bound only guarantees
       // that a wave always finishes).
       for (int spin = 0; spin < (1 << 22); ++spin) {
-        try_claim(ui);
-        mark_ready();
+        if (!try_claim(ui)) __builtin_amdgcn_s_sleep(1);
         if (is_ready(ui)) break;
-        __builtin_amdgcn_s_sleep(1);
       }
     }
 
@@ -630,6 +647,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       __hip_atomic_fetch_add(&s_done[ui % LS_ATT_STAGES], 1u, __ATOMIC_RELEASE,
                              __HIP_MEMORY_SCOPE_WORKGROUP);
   }
+  LS_WAIT_VMCNT(0);  // no copy of this wave may land after the workgroup ends
 
   // ---- epilogue ----
 #pragma unroll
@@ -678,7 +696,7 @@ __global__ __launch_bounds__(64) void ls_bias_kernel(const typename LsElem<CT>::
 // ---------------------------------------------------------------------------
 namespace {
 struct AttnWs {
-  size_t vt, pg, tiles, vexp, cb, total;
+  size_t vt, pg, tiles, vexp, cb, tok, total;
   int64_t lpad, n_pages;
 };
 AttnWs attn_ws(int64_t total_k, int batch, int G, int D, int eb, bool bias) {
@@ -691,6 +709,7 @@ AttnWs attn_ws(int64_t total_k, int batch, int G, int D, int eb, bool bias) {
   L.tiles = off; off += ls_align256((size_t)(batch + 1) * 4);
   L.vexp = off; off += ls_align256((size_t)G * L.n_pages * 4);
   L.cb = off; off += bias ? ls_align256((size_t)G * L.lpad * 4) : 0;
+  L.tok = off; off += ls_align256((size_t)(LS_ATT_MAX_UNION + 1) * 4);
   L.total = off;
   return L;
 }
@@ -698,12 +717,13 @@ AttnWs attn_ws(int64_t total_k, int batch, int G, int D, int eb, bool bias) {
 template <int DT, bool BIAS>
 void launch_tile(dim3 grid, hipStream_t s, const void* q, int64_t q_rs, const void* k, int64_t k_rs,
                  const uint16_t* vt, const AttnWs& L, const int32_t* vexp, const float* cb,
+                 const int32_t* tok,
                  const int32_t* cu_q, const int32_t* cu_k, const int32_t* pg,
                  const int32_t* tiles, int batch, int64_t total_q, int G, int gs,
                  const int32_t* topk_idx, int take, float scale_log2, int causal, void* out,
                  float* lse) {
   hipLaunchKernelGGL((ls_attn_tile_kernel<DT, BIAS>), grid, dim3(LS_ATT_THREADS), 0, s,
-                     (const uint16_t*)q, q_rs, (const uint16_t*)k, k_rs, vt, L.lpad, vexp, cb,
+                     (const uint16_t*)q, q_rs, (const uint16_t*)k, k_rs, vt, L.lpad, vexp, cb, tok,
                      L.n_pages, cu_q, cu_k, pg, tiles, batch, total_q, G, gs, topk_idx, take,
                      scale_log2, causal, (uint16_t*)out, lse, (int)(grid.x / 8));
 }
@@ -753,8 +773,9 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   int32_t* vexp = (int32_t*)(ws + L.vexp);
   int32_t* tiles = (int32_t*)(ws + L.tiles);
   float* cb = bias ? (float*)(ws + L.cb) : nullptr;
+  int32_t* tok = (int32_t*)(ws + L.tok);
   hipLaunchKernelGGL(ls_attn_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens_q, cu_seqlens_k,
-                     batch, LS_ATT_TILE, pg, tiles);
+                     batch, LS_ATT_TILE, pg, tiles, tok, LS_ATT_MAX_UNION + 1);
   int rc = ls_check_launch("ls_attn_plan_kernel");
   if (rc) return rc;
   if (total_k > 0) {
@@ -785,7 +806,7 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   const int64_t tile_bound = (total_q + LS_ATT_TILE - 1) / LS_ATT_TILE + batch;
   const dim3 grid((unsigned)(8 * ((tile_bound + 7) / 8)), num_kv_heads, (gs + 15) / 16);
 #define LS_TILE_ARGS                                                                              \
-  grid, s, q, q_row_stride, k, k_row_stride, vt, L, vexp, cb, cu_seqlens_q, cu_seqlens_k, pg,     \
+  grid, s, q, q_row_stride, k, k_row_stride, vt, L, vexp, cb, tok, cu_seqlens_q, cu_seqlens_k, pg,\
       tiles, batch, total_q, num_kv_heads, gs, topk_idx, take, scale_log2, causal, out, lse
   if (dtype == LS_BF16) {
     if (bias) launch_tile<LS_BF16, true>(LS_TILE_ARGS);
