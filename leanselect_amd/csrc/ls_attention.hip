@@ -237,10 +237,12 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   // The per-row page bitmaps are only needed before streaming starts and
   // share their LDS with the ring.
   __shared__ __align__(16) uint8_t s_ring[LS_ATT_STAGES * LS_ATT_STAGE_BYTES];
-  __shared__ uint16_t s_union[LS_ATT_MAX_UNION];
-  __shared__ int8_t s_uexp[LS_ATT_MAX_UNION];
-  __shared__ uint32_t s_umask[LS_ATT_MAX_UNION];
+  // Union entry: page << 16 | mask of the tile rows that selected it.
+  __shared__ uint32_t s_umeta[LS_ATT_MAX_UNION];
   __shared__ uint8_t s_uneed[LS_ATT_MAX_UNION];  // waves with a row on the page
+  // Bit u of s_wneed[w] is set when a row of wave w selected union page u.
+  __shared__ uint32_t s_wneed[LS_ATT_WAVES][LS_ATT_MAX_UNION / 32];
+  __shared__ int32_t s_sexp[LS_ATT_STAGES];  // V exponent of the page in each stage
   __shared__ int s_wsum[LS_ATT_WAVES];
   // Ring protocol: s_next = next union page to be claimed for copying;
   // s_ready[st] = union index + 1 of the page whose copy into stage st has
@@ -289,8 +291,35 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       tile_jmax >= 0 ? (int)min(tile_jmax / 64, (int64_t)LS_ATTN_MAX_PAGES - 1) : -1;
   const int nwords = last_page / 32 + 1;
 
+  // ---- per-row state: Q^T fragments (B operand), softmax stats, O^T ----
+  // (the Q loads are issued first; they land while the page list is built)
+  ls_u32x4 qf[LS_ATT_TPW][4];
+  // m_run: running max in scaled base-2 units (score * scale_log2); thr: the
+  // raw score above which a key would exceed m_run by more than 2^8.
+  float m_run[LS_ATT_TPW], l_run[LS_ATT_TPW], thr[LS_ATT_TPW];
+  int jmax_r[LS_ATT_TPW];
+  ls_f32x4 o[LS_ATT_TPW][8];
+#pragma unroll
+  for (int j = 0; j < LS_ATT_TPW; ++j) {
+    const int row = w * LS_ATT_TPW + j;
+    const int64_t t = t0 + min(row, n_rows - 1);
+    const uint16_t* qrow = qg + t * q_rs + ((int64_t)g * gs + (head_ok ? head : 0)) * D + 8 * q;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      qf[j][ks] = ls_load16(qrow + 32 * ks);
+      if (!head_ok) qf[j][ks] = ls_u32x4{0u, 0u, 0u, 0u};
+    }
+    m_run[j] = -INFINITY;
+    l_run[j] = 0.f;
+    thr[j] = -INFINITY;
+    jmax_r[j] = row < n_rows ? (int)row_jmax(row) : -1;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) o[j][db] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   // ---- per-row page bitmaps and their sorted union ----
   for (int i = tid; i < LS_ATT_TILE * nwords; i += LS_ATT_THREADS) s_bits[i / nwords][i % nwords] = 0u;
+  for (int i = tid; i < LS_ATT_WAVES * (LS_ATT_MAX_UNION / 32); i += LS_ATT_THREADS)
+    s_wneed[i / (LS_ATT_MAX_UNION / 32)][i % (LS_ATT_MAX_UNION / 32)] = 0u;
   if (tid < LS_ATT_STAGES) {
     s_ready[tid] = 0u;
     s_done[tid] = 0u;
@@ -308,10 +337,11 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     }
   }
   __syncthreads();
-  uint32_t word = 0u;
-  if (tid < nwords) {
+  uint32_t word = 0u, row_word[LS_ATT_TILE];
 #pragma unroll
-    for (int i = 0; i < LS_ATT_TILE; ++i) word |= s_bits[i][tid];
+  for (int i = 0; i < LS_ATT_TILE; ++i) {
+    row_word[i] = tid < nwords ? s_bits[i][tid] : 0u;
+    word |= row_word[i];
   }
   int wtot;
   const int wpos = ls_wave_excl_scan(__popc(word), lane, &wtot);
@@ -351,53 +381,28 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     const int page = tid * 32 + bit;
     uint32_t rows = 0u;
 #pragma unroll
-    for (int i = 0; i < LS_ATT_TILE; ++i) rows |= ((s_bits[i][tid] >> bit) & 1u) << i;
+    for (int i = 0; i < LS_ATT_TILE; ++i) rows |= ((row_word[i] >> bit) & 1u) << i;
     const int dst = (int)(((uint32_t)pos * (uint32_t)stride) % (uint32_t)n_union);
     int n_waves = 0;
 #pragma unroll
-    for (int i = 0; i < LS_ATT_WAVES; ++i) n_waves += ((rows >> (LS_ATT_TPW * i)) & ROWS_MASK) != 0u;
-    s_uexp[dst] = (int8_t)vexp_seq[page];
-    s_umask[dst] = rows;
+    for (int i = 0; i < LS_ATT_WAVES; ++i) {
+      if (((rows >> (LS_ATT_TPW * i)) & ROWS_MASK) != 0u) {
+        ++n_waves;
+        atomicOr(&s_wneed[i][dst >> 5], 1u << (dst & 31));
+      }
+    }
+    s_umeta[dst] = ((uint32_t)page << 16) | rows;
     s_uneed[dst] = (uint8_t)n_waves;
-    s_union[dst] = (uint16_t)page;
     ++pos;
   }
 
-  // ---- per-row state: Q^T fragments (B operand), softmax stats, O^T ----
-  ls_u32x4 qf[LS_ATT_TPW][4];
-  // m_run: running max in scaled base-2 units (score * scale_log2); thr: the
-  // raw score above which a key would exceed m_run by more than 2^8.
-  float m_run[LS_ATT_TPW], l_run[LS_ATT_TPW], thr[LS_ATT_TPW];
-  int jmax_r[LS_ATT_TPW];
-  ls_f32x4 o[LS_ATT_TPW][8];
-#pragma unroll
-  for (int j = 0; j < LS_ATT_TPW; ++j) {
-    const int row = w * LS_ATT_TPW + j;
-    const int64_t t = t0 + min(row, n_rows - 1);
-    const uint16_t* qrow = qg + t * q_rs + ((int64_t)g * gs + (head_ok ? head : 0)) * D + 8 * q;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      qf[j][ks] = ls_load16(qrow + 32 * ks);
-      if (!head_ok) qf[j][ks] = ls_u32x4{0u, 0u, 0u, 0u};
-    }
-    m_run[j] = -INFINITY;
-    l_run[j] = 0.f;
-    thr[j] = -INFINITY;
-    jmax_r[j] = row < n_rows ? (int)row_jmax(row) : -1;
-#pragma unroll
-    for (int db = 0; db < 8; ++db) o[j][db] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  __syncthreads();  // union list, exponents and every wave's Q loads are complete;
-                    // the bitmaps are dead, so the ring may be written
+  __syncthreads();  // the union list is complete and the bitmaps are dead, so
+                    // the ring may be written
   LS_WAIT_VMCNT(0);
   // This wave's pages: bit b of lane l is set when one of its rows selected
   // union page 32 l + b (the union holds at most 64 x 32 pages).
   static_assert(LS_ATT_MAX_UNION <= 64 * 32, "one need word per lane");
-  uint32_t wneed = 0u;
-  for (int b = 0; b < 32; ++b) {
-    const int u = 32 * lane + b;
-    if (u < n_union && ((s_umask[u] >> (LS_ATT_TPW * w)) & ROWS_MASK) != 0u) wneed |= 1u << b;
-  }
+  const uint32_t wneed = lane < LS_ATT_MAX_UNION / 32 ? s_wneed[w][lane] : 0u;
 
   // ---- staging ----
   // One wave copies a whole union page into its stage: K as 64 rows of 256 B
@@ -437,7 +442,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   for (int m = 0; m < 2; ++m)
     v_lane[m] = (uint32_t)((lane >> 3) * 2 * lpad) + 16u * (uint32_t)((lane & 7) ^ (4 * m + l4));
   auto issue_page = [&](int ui_copy) {
-    const int page = __builtin_amdgcn_readfirstlane((int)s_union[ui_copy]);
+    const int page = __builtin_amdgcn_readfirstlane((int)(s_umeta[ui_copy] >> 16));
     const uint32_t kb = ring_off + (ui_copy % LS_ATT_STAGES) * LS_ATT_STAGE_BYTES;
     const uint32_t vb = kb + LS_ATT_KBYTES;
     // Keys past the sequence end repeat its last key (their scores are masked).
@@ -466,10 +471,13 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       if (lane < 16)
         ls_dma16(cgrp + 64LL * page, 16u * (uint32_t)lane,
                  (uint32_t)(uintptr_t)(ls_lds_void*)s_bias + (ui_copy % LS_ATT_STAGES) * 256u);
-    // Last: the ready token ui_copy + 1 into s_ready[stage] (lane 0 only).
-    if (lane == 0)
+    // The page's V exponent, then last the ready token ui_copy + 1 (lane 0 only).
+    if (lane == 0) {
+      ls_dma4(vexp_seq + page, 0u,
+              (uint32_t)(uintptr_t)(ls_lds_void*)&s_sexp[ui_copy % LS_ATT_STAGES]);
       ls_dma4(tok + ui_copy + 1, 0u,
               (uint32_t)(uintptr_t)(ls_lds_void*)&s_ready[ui_copy % LS_ATT_STAGES]);
+    }
   };
   // Hands stage u % 4 to page u (its waves count from zero) and copies it.
   auto issue_copy = [&](int u) {
@@ -508,7 +516,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   };
 
   auto compute_page = [&](int ui, int page, uint32_t sel) {
-    const int v_e = s_uexp[ui];
+    const int v_e = s_sexp[ui % LS_ATT_STAGES];
     const float p_unscale = __builtin_ldexpf(1.f, -v_e);
     const uint8_t* kb = s_ring + (ui % LS_ATT_STAGES) * LS_ATT_STAGE_BYTES;
     const uint8_t* vb = kb + LS_ATT_KBYTES;
@@ -629,7 +637,10 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     const int L = (int)__builtin_ctzll(lanes);
     return 32 * L + (int)__builtin_ctz((uint32_t)__builtin_amdgcn_readlane((int)word, L));
   };
-  for (int ui = next_page(-1); ui < n_union; ui = next_page(ui)) {
+  // The next page's union entry is read before the current page is computed.
+  int ui = next_page(-1);
+  uint32_t meta = ui < n_union ? s_umeta[ui] : 0u;
+  while (ui < n_union) {
     if (!is_ready(ui)) {
       // Bounded wait (the protocol cannot deadlock; the bound only guarantees
       // that a wave always finishes).
@@ -639,13 +650,16 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       }
     }
 
-    const int page = s_union[ui];
-    const uint32_t sel = __builtin_amdgcn_readfirstlane((s_umask[ui] >> (LS_ATT_TPW * w)) & ROWS_MASK);
-    compute_page(ui, page, sel);
+    const int nxt = next_page(ui);
+    const uint32_t meta_next = nxt < n_union ? s_umeta[nxt] : 0u;
+    const uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)meta);
+    compute_page(ui, (int)(m >> 16), (m >> (LS_ATT_TPW * w)) & ROWS_MASK);
     // Done with the stage (the release orders this wave's reads of it first).
     if (lane == 0)
       __hip_atomic_fetch_add(&s_done[ui % LS_ATT_STAGES], 1u, __ATOMIC_RELEASE,
                              __HIP_MEMORY_SCOPE_WORKGROUP);
+    ui = nxt;
+    meta = meta_next;
   }
   LS_WAIT_VMCNT(0);  // no copy of this wave may land after the workgroup ends
 
