@@ -35,6 +35,9 @@ HIPCC_FLAGS = [
 # canonicalising moves and fuse into v_max3.
 FILE_FLAGS = {
     "ls_attention": ["-mno-amdgpu-ieee", "-fno-honor-nans"],
+    # MFMAs accumulate in ordinary VGPRs, so their results need no copies out
+    # of the accumulation registers before the pooling reads them.
+    "ls_select": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -314,34 +314,33 @@ __global__ __launch_bounds__(256) void ls_score_mfma_kernel(
   const uint16_t* kbase = kt + ((int64_t)g * Na + a0) * F + 8 * q;
   float carry[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   const int j_first = jw_lo > 0 ? jw_lo - 1 : 0;  // one step early primes the carry
-  ls_u32x4 kf[KS];
-  {
-    const uint16_t* kp = kbase + min((int64_t)16 * j_first + r, n_atoms - 1) * F;
+  const int n_at = (int)n_atoms;
+  auto load_k = [&](ls_u32x4 (&kf)[KS], int j) {
+    const uint16_t* kp = kbase + (int64_t)min(16 * j + r, n_at - 1) * F;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kf[ks] = ls_load16(kp + 32 * ks);
-  }
-  for (int j = j_first; j <= jw_hi; ++j) {
-    ls_u32x4 kn[KS];
-    if (j < jw_hi) {  // prefetch the next step's k~ rows
-      const uint16_t* kp = kbase + min((int64_t)16 * (j + 1) + r, n_atoms - 1) * F;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kn[ks] = ls_load16(kp + 32 * ks);
-    }
+  };
+  // One 16-atom step on k~ fragments kc, prefetching the next step's into kn.
+  auto step = [&](int j, const ls_u32x4 (&kc)[KS], ls_u32x4 (&kn)[KS]) {
+    if (j < jw_hi) load_k(kn, j + 1);
     ls_f32x4 acc[4];
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
       acc[tb] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) acc[tb] = LsElem<DT>::mfma(kf[ks], qf[tb][ks], acc[tb]);
+      for (int ks = 0; ks < KS; ++ks) acc[tb] = LsElem<DT>::mfma(kc[ks], qf[tb][ks], acc[tb]);
     }
-    const int64_t atom0 = (int64_t)16 * j + 4 * q;
+    const int atom0 = 16 * j + 4 * q;
     const int p = 4 * j + q;
     const bool write = j >= jw_lo && p >= p_lo && p <= p_hi;
+    const bool tail = 16 * j + 15 >= n_at;  // uniform: only the last step has atoms past the end
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
+      if (tail) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (atom0 + i >= n_atoms) acc[tb][i] = -INFINITY;
+        for (int i = 0; i < 4; ++i)
+          if (atom0 + i >= n_at) acc[tb][i] = -INFINITY;
+      }
       const float m4 = fmaxf(fmaxf(acc[tb][0], acc[tb][1]), fmaxf(acc[tb][2], acc[tb][3]));
       const float rot = ls_shfl(acc[tb][3], (lane - 16) & 63);
       const float prev = q == 0 ? carry[tb] : rot;
@@ -349,11 +348,16 @@ __global__ __launch_bounds__(256) void ls_score_mfma_kernel(
       if (write && tok_ok[tb])
         out[((int64_t)g * Nq + tok[tb]) * out_stride + p] = LsElem<DT>::from_f(fmaxf(m4, prev));
     }
-    if (j < jw_hi) {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[ks] = kn[ks];
-    }
+  };
+  // Two fragment buffers used in turn (no register copies between steps).
+  ls_u32x4 kA[KS], kB[KS];
+  load_k(kA, j_first);
+  int j = j_first;
+  for (; j + 1 <= jw_hi; j += 2) {
+    step(j, kA, kB);
+    step(j + 1, kB, kA);
   }
+  if (j <= jw_hi) step(j, kA, kB);
 }
 
 // float32 page scores on the vector ALU: one thread per (group, token, page).
