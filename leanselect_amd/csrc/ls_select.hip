@@ -254,7 +254,7 @@ __global__ void ls_select_plan_kernel(const int32_t* __restrict__ cu_q, int batc
 #define LS_SCORE_ALL 2
 
 template <int DT, int KS, int MODE>
-__global__ __launch_bounds__(256) void ls_score_mfma_kernel(
+__global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_mfma_kernel(
     const uint16_t* __restrict__ qt, int64_t Nq, const uint16_t* __restrict__ kt, int64_t Na,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_a,
     const int32_t* __restrict__ blk_off, int batch, int64_t n_blk_launch, int init_blocks,
@@ -320,9 +320,13 @@ __global__ __launch_bounds__(256) void ls_score_mfma_kernel(
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kf[ks] = ls_load16(kp + 32 * ks);
   };
-  // One 16-atom step on k~ fragments kc, prefetching the next step's into kn.
+  // Prefetch distance in steps: two where a third fragment buffer fits in the
+  // register budget, one for the widest routers.
+  constexpr int PD = KS <= 6 ? 2 : 1;
+  // One 16-atom step on k~ fragments kc, prefetching the fragments of step
+  // j + PD into kn.
   auto step = [&](int j, const ls_u32x4 (&kc)[KS], ls_u32x4 (&kn)[KS]) {
-    if (j < jw_hi) load_k(kn, j + 1);
+    if (j + PD <= jw_hi) load_k(kn, j + PD);
     ls_f32x4 acc[4];
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
@@ -349,15 +353,28 @@ __global__ __launch_bounds__(256) void ls_score_mfma_kernel(
         out[((int64_t)g * Nq + tok[tb]) * out_stride + p] = LsElem<DT>::from_f(fmaxf(m4, prev));
     }
   };
-  // Two fragment buffers used in turn (no register copies between steps).
-  ls_u32x4 kA[KS], kB[KS];
-  load_k(kA, j_first);
+  // PD + 1 fragment buffers used in turn (no register copies between steps).
   int j = j_first;
-  for (; j + 1 <= jw_hi; j += 2) {
-    step(j, kA, kB);
-    step(j + 1, kB, kA);
+  if constexpr (PD == 2) {
+    ls_u32x4 kA[KS], kB[KS], kC[KS];
+    load_k(kA, j_first);
+    if (j_first < jw_hi) load_k(kB, j_first + 1);
+    for (; j + 2 <= jw_hi; j += 3) {
+      step(j, kA, kC);
+      step(j + 1, kB, kA);
+      step(j + 2, kC, kB);
+    }
+    if (j <= jw_hi) step(j, kA, kC);
+    if (j + 1 <= jw_hi) step(j + 1, kB, kA);
+  } else {
+    ls_u32x4 kA[KS], kB[KS];
+    load_k(kA, j_first);
+    for (; j + 1 <= jw_hi; j += 2) {
+      step(j, kA, kB);
+      step(j + 1, kB, kA);
+    }
+    if (j <= jw_hi) step(j, kA, kB);
   }
-  if (j <= jw_hi) step(j, kA, kB);
 }
 
 // float32 page scores on the vector ALU: one thread per (group, token, page).
