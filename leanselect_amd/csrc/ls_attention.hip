@@ -74,72 +74,15 @@ __global__ void ls_attn_plan_kernel(const int32_t* __restrict__ cu_q,
   }
 }
 
-// vt[g][d][64 * pg_off[b] + j] = fp16(v[cu_k[b] + j][g][d] * 2^-e)  (0 for j >= len_k(b)),
-// vexp[g * n_pages + pg_off[b] + p] = e: the smallest e >= 0 (at most 15) that keeps
-// the page's scaled values within +-32768, so they are finite in fp16 (e = 0 for
-// ordinary activations; bf16 values are then exact in fp16 down to 2^-14).
-// One workgroup transposes one 64-key page of one group through LDS.
-template <int DT, int D>
-__global__ __launch_bounds__(256) void ls_vt_kernel(const uint16_t* __restrict__ v,
-                                                    int64_t v_rs, const int32_t* __restrict__ cu_k,
-                                                    const int32_t* __restrict__ pg_off,
-                                                    int batch, int64_t lpad, int64_t n_pages,
-                                                    uint16_t* __restrict__ vt,
-                                                    int32_t* __restrict__ vexp) {
-  constexpr int PITCH = D + 2;
-  __shared__ uint16_t tile[64 * PITCH];
-  __shared__ float wave_max[4];
-  const int64_t tile_id = LS_BID_X;
-  if (tile_id >= pg_off[batch]) return;
-  const int g = LS_BID_Y;
-  const int b = ls_find_segment(pg_off, batch, tile_id);
-  const int p = (int)(tile_id - pg_off[b]);
-  const int lk = cu_k[b + 1] - cu_k[b];
-  const int64_t krow0 = (int64_t)cu_k[b] + 64LL * p;
-  constexpr int CH = D / 8;  // 16-byte chunks per row
-  float mx = 0.f;
-  for (int c = LS_TID; c < 64 * CH; c += 256) {
-    const int key = c / CH, d0 = (c % CH) * 8;
-    ls_u32x4 val = {0u, 0u, 0u, 0u};
-    if (64 * p + key < lk) val = ls_load16(v + (krow0 + key) * v_rs + (int64_t)g * D + d0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint16_t lo = (uint16_t)(val[i] & 0xffffu), hi = (uint16_t)(val[i] >> 16);
-      mx = fmaxf(mx, fmaxf(fabsf(LsElem<DT>::to_f(lo)), fabsf(LsElem<DT>::to_f(hi))));
-      tile[key * PITCH + d0 + 2 * i] = lo;
-      tile[key * PITCH + d0 + 2 * i + 1] = hi;
-    }
-  }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, LS_WAVE));
-  if ((LS_TID & 63) == 0) wave_max[LS_TID >> 6] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
-  int e = 0;
-  while (e < 15 && mx * __builtin_ldexpf(1.f, -e) > 32768.f) ++e;
-  const float scale = __builtin_ldexpf(1.f, -e);
-  if (LS_TID == 0) vexp[(int64_t)g * n_pages + pg_off[b] + p] = e;
-  const int64_t col0 = 64LL * (pg_off[b] + p);
-  for (int c = LS_TID; c < D * 8; c += 256) {
-    const int d = c / 8, k0 = (c % 8) * 8;
-    ls_u32x4 o;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      o[i] = ls_pack2(ls_f32_to_f16(LsElem<DT>::to_f(tile[(k0 + 2 * i) * PITCH + d]) * scale),
-                      ls_f32_to_f16(LsElem<DT>::to_f(tile[(k0 + 2 * i + 1) * PITCH + d]) * scale));
-    *reinterpret_cast<ls_u32x4*>(vt + ((int64_t)g * D + d) * lpad + col0 + k0) = o;
-  }
-}
-
 // ---------------------------------------------------------------------------
-// Tile kernel: one workgroup = 32 consecutive query rows of one sequence and
-// one KV group (4 waves x 8 rows, one wave per SIMD).  The rows' page plans
-// are OR-ed into a sorted union page list; each union page of K and V^T is
-// streamed once into a 4-stage LDS ring with direct global->LDS loads issued
-// three pages ahead, and every row that selected the page runs its MFMAs on
-// it.  Rows that did not select a page skip it (no masked-out work).  A wave
-// keeps its eight rows' O^T accumulators (8 x 32 floats per lane) in the
-// accumulation registers and their Q^T fragments in vector registers.
+// Tile kernel: one workgroup = LS_ATT_TILE (16) consecutive query rows of one
+// sequence and one KV group for 16 of its query heads (8 waves x 2 rows, two
+// waves per SIMD).  The rows' page plans are OR-ed into a union page list;
+// each union page of staged K and V^T is streamed once into a 4-stage LDS ring
+// with direct global->LDS loads, and every row that selected the page runs its
+// MFMAs on it.  Rows that did not select a page skip it (no masked-out work).
+// A wave keeps its two rows' O^T accumulators (2 x 8 x 4 floats per lane) and
+// Q^T fragments in registers.
 // ---------------------------------------------------------------------------
 #ifndef LS_ATT_TPW
 #define LS_ATT_TPW 2                         // rows per wave
@@ -166,6 +109,78 @@ typedef float ls_float2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ int ls_att_key_of_row(int row) {
   const int c = row >> 5, rr = row & 31, nb = rr >> 4, r = rr & 15;
   return 32 * c + 8 * (r >> 2) + 4 * nb + (r & 3);
+}
+
+// Page-major staging of K and V in the ring's own byte order: block
+// kv[g][pg_off[b] + p] (LS_ATT_STAGE_BYTES) holds page p of sequence b, group
+// g, exactly as a ring stage holds it, so a page copy is one contiguous
+// 32 KB transfer:
+//  - bytes [0, 16K): K, 64 rows of 256 B; row R holds key ls_att_key_of_row(R)
+//    of the page, its 16-byte chunk C (dims 8C..8C+7) at position C ^ (R & 15);
+//  - bytes [16K, 32K): V^T, 128 rows of 128 B; row d holds fp16(v[key][d] * 2^-e)
+//    of the page's 64 keys, chunk C (keys 8C..8C+7) at position C ^ ((d >> 1) & 7).
+// Keys past the sequence end are zero (their scores are always masked).
+// vexp[g * n_pages + pg_off[b] + p] = e: the smallest e >= 0 (at most 15) that
+// keeps the page's scaled V within +-32768, so it is finite in fp16 (e = 0 for
+// ordinary activations; bf16 values are then exact in fp16 down to 2^-14).
+// One workgroup stages one page of one group (V^T goes through LDS).
+template <int DT>
+__global__ __launch_bounds__(256) void ls_kv_stage_kernel(
+    const uint16_t* __restrict__ k, int64_t k_rs, const uint16_t* __restrict__ v, int64_t v_rs,
+    const int32_t* __restrict__ cu_k, const int32_t* __restrict__ pg_off, int batch,
+    int64_t n_pages, uint8_t* __restrict__ kv, int32_t* __restrict__ vexp) {
+  constexpr int D = 128, PITCH = D + 2, CH = D / 8;
+  __shared__ uint16_t tile[64 * PITCH];
+  __shared__ float wave_max[4];
+  const int64_t tile_id = LS_BID_X;
+  if (tile_id >= pg_off[batch]) return;
+  const int g = LS_BID_Y;
+  const int b = ls_find_segment(pg_off, batch, tile_id);
+  const int p = (int)(tile_id - pg_off[b]);
+  const int lk = cu_k[b + 1] - cu_k[b];
+  const int64_t krow0 = (int64_t)cu_k[b] + 64LL * p;
+  uint8_t* blk = kv + ((int64_t)g * n_pages + pg_off[b] + p) * LS_ATT_STAGE_BYTES;
+  // K: output chunk o = 16 R + position.
+  for (int o = LS_TID; o < 64 * CH; o += 256) {
+    const int R = o >> 4, C = (o & 15) ^ (R & 15);
+    const int key = ls_att_key_of_row(R);
+    ls_u32x4 val = {0u, 0u, 0u, 0u};
+    if (64 * p + key < lk) val = ls_load16(k + (krow0 + key) * k_rs + (int64_t)g * D + 8 * C);
+    *reinterpret_cast<ls_u32x4*>(blk + 16 * o) = val;
+  }
+  // V through LDS, then V^T rows.
+  float mx = 0.f;
+  for (int c = LS_TID; c < 64 * CH; c += 256) {
+    const int key = c / CH, d0 = (c % CH) * 8;
+    ls_u32x4 val = {0u, 0u, 0u, 0u};
+    if (64 * p + key < lk) val = ls_load16(v + (krow0 + key) * v_rs + (int64_t)g * D + d0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = (uint16_t)(val[i] & 0xffffu), hi = (uint16_t)(val[i] >> 16);
+      mx = fmaxf(mx, fmaxf(fabsf(LsElem<DT>::to_f(lo)), fabsf(LsElem<DT>::to_f(hi))));
+      tile[key * PITCH + d0 + 2 * i] = lo;
+      tile[key * PITCH + d0 + 2 * i + 1] = hi;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, LS_WAVE));
+  if ((LS_TID & 63) == 0) wave_max[LS_TID >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
+  int e = 0;
+  while (e < 15 && mx * __builtin_ldexpf(1.f, -e) > 32768.f) ++e;
+  const float scale = __builtin_ldexpf(1.f, -e);
+  if (LS_TID == 0) vexp[(int64_t)g * n_pages + pg_off[b] + p] = e;
+  uint8_t* vblk = blk + LS_ATT_KBYTES;
+  for (int c = LS_TID; c < D * 8; c += 256) {
+    const int d = c / 8, k0 = (c % 8) * 8;
+    ls_u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = ls_pack2(ls_f32_to_f16(LsElem<DT>::to_f(tile[(k0 + 2 * i) * PITCH + d]) * scale),
+                      ls_f32_to_f16(LsElem<DT>::to_f(tile[(k0 + 2 * i + 1) * PITCH + d]) * scale));
+    *reinterpret_cast<ls_u32x4*>(vblk + d * 128 + 16 * ((c % 8) ^ ((d >> 1) & 7))) = o;
+  }
 }
 
 // One 16-byte global->LDS load per lane from sbase + voff bytes (lane l lands
@@ -223,8 +238,7 @@ __device__ __forceinline__ float ls_sum_f16x2(uint32_t x, float acc) {
 // staged like V^T and copied with each page (256 B per stage).
 template <int DT, bool BIAS>
 __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_tile_kernel(
-    const uint16_t* __restrict__ qg, int64_t q_rs, const uint16_t* __restrict__ kg,
-    int64_t k_rs, const uint16_t* __restrict__ vt, int64_t lpad,
+    const uint16_t* __restrict__ qg, int64_t q_rs, const uint8_t* __restrict__ kv, int64_t lpad,
     const int32_t* __restrict__ vexp, const float* __restrict__ cb,
     const int32_t* __restrict__ tok, int64_t n_pages_ws,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
@@ -277,7 +291,6 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   const int n_rows = (int)min((int64_t)LS_ATT_TILE, (int64_t)cu_q[b + 1] - t0);
   const int lq = cu_q[b + 1] - cu_q[b];
   const int lk = cu_k[b + 1] - cu_k[b];
-  const int64_t kstart = cu_k[b];
   const int64_t vbase = 64LL * pg_off[b];
   const int64_t tr0 = t0 - cu_q[b];
   // Keys visible to row i of the tile: j <= jmax(i) (the last row sees the most).
@@ -405,11 +418,11 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   const uint32_t wneed = lane < LS_ATT_MAX_UNION / 32 ? s_wneed[w][lane] : 0u;
 
   // ---- staging ----
-  // One wave copies a whole union page into its stage: K as 64 rows of 256 B
-  // (row R holds key ls_att_key_of_row(R), 16-byte chunk C at position
-  // C ^ (R & 15)) and V^T as 128 rows of 128 B (chunk C at C ^ ((d >> 1) & 7)),
-  // so the sixteen lanes of an MFMA operand read hit sixteen distinct bank
-  // groups.  Each copy fills 1 KB of contiguous LDS (lane l -> byte 16 l).
+  // One wave copies a whole union page into its stage: the page's staged
+  // block (K rows with chunk C of row R at position C ^ (R & 15), V^T rows
+  // with chunk C of row d at C ^ ((d >> 1) & 7), so the sixteen lanes of an
+  // MFMA operand read hit sixteen distinct bank groups) is copied byte for
+  // byte, 1 KB per load (lane l -> byte 16 l).
   //
   // Waves are not kept in lockstep, and a wave visits only the pages its rows
   // selected, waiting only for the page it is about to read.  Union page u
@@ -423,49 +436,18 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   // bias.  Computing waves never copy (the last wave on a page is often the
   // slowest one).  A page's copy depends only on earlier pages being
   // finished, so every wait ends.
-  const uint16_t* kgrp = kg + (int64_t)g * D;
-  const uint16_t* vgrp = vt + (int64_t)g * D * lpad + vbase;
+  const uint8_t* kvgrp = kv + ((int64_t)g * n_pages_ws + pg_off[b]) * LS_ATT_STAGE_BYTES;
   const float* cgrp = BIAS ? cb + (int64_t)g * lpad + vbase : nullptr;
   const uint32_t ring_off = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(ls_lds_void*)s_ring);
-  const int64_t k_rs_bytes = 2 * k_rs;
-  // Lane parts of the copy offsets (page-independent): K copy i covers rows
-  // 4i..4i+3, so R & 15 = 4 (i & 3) + l4 and the key is kbase(i) + l4; V^T copy
-  // i covers rows 8i..8i+7, so (d >> 1) & 7 = 4 (i & 1) + l4.  The i-dependent
-  // row offsets go into the scalar base.
-  const int l4 = lane >> 4;
-  uint32_t k_lane[4], v_lane[2];
-#pragma unroll
-  for (int m = 0; m < 4; ++m)
-    k_lane[m] = (uint32_t)(l4 * k_rs_bytes) + 16u * (uint32_t)((lane & 15) ^ (4 * m + l4));
-#pragma unroll
-  for (int m = 0; m < 2; ++m)
-    v_lane[m] = (uint32_t)((lane >> 3) * 2 * lpad) + 16u * (uint32_t)((lane & 7) ^ (4 * m + l4));
   auto issue_page = [&](int ui_copy) {
     const int page = __builtin_amdgcn_readfirstlane((int)(s_umeta[ui_copy] >> 16));
     const uint32_t kb = ring_off + (ui_copy % LS_ATT_STAGES) * LS_ATT_STAGE_BYTES;
-    const uint32_t vb = kb + LS_ATT_KBYTES;
-    // Keys past the sequence end repeat its last key (their scores are masked).
-    const int key_rem = lk - 1 - 64 * page;  // >= 0: every union page is visible
-    const uint16_t* kpage = kgrp + (kstart + 64LL * page) * k_rs;
-    if (key_rem >= 63) {
+    // The staged page is the stage's byte image: 32 contiguous 1 KB copies.
+    const uint8_t* src = kvgrp + (int64_t)page * LS_ATT_STAGE_BYTES;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kbase = 32 * (i >> 3) + 8 * (i & 3) + 4 * ((i >> 2) & 1);
-        ls_dma16(kpage + (int64_t)kbase * k_rs, k_lane[i & 3], kb + i * 1024);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kbase = 32 * (i >> 3) + 8 * (i & 3) + 4 * ((i >> 2) & 1);
-        const int key = min(kbase + l4, key_rem);
-        const uint32_t voff = (uint32_t)(key * k_rs_bytes) + (k_lane[i & 3] - (uint32_t)(l4 * k_rs_bytes));
-        ls_dma16(kpage, voff, kb + i * 1024);
-      }
-    }
-    const uint16_t* vpage = vgrp + 64LL * page;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) ls_dma16(vpage + 8LL * i * lpad, v_lane[i & 1], vb + i * 1024);
+    for (int i = 0; i < LS_ATT_STAGE_BYTES / 1024; ++i)
+      ls_dma16(src + 1024 * i, 16u * (uint32_t)lane, kb + i * 1024);
     // The page's 64 biases (lanes 0..15, 16 bytes each).
     if constexpr (BIAS)
       if (lane < 16)
@@ -710,15 +692,15 @@ __global__ __launch_bounds__(64) void ls_bias_kernel(const typename LsElem<CT>::
 // ---------------------------------------------------------------------------
 namespace {
 struct AttnWs {
-  size_t vt, pg, tiles, vexp, cb, tok, total;
+  size_t kv, pg, tiles, vexp, cb, tok, total;
   int64_t lpad, n_pages;
 };
-AttnWs attn_ws(int64_t total_k, int batch, int G, int D, int eb, bool bias) {
+AttnWs attn_ws(int64_t total_k, int batch, int G, bool bias) {
   AttnWs L;
   L.n_pages = (total_k + 63) / 64 + batch;
   L.lpad = L.n_pages * 64;
   size_t off = 0;
-  L.vt = off; off += ls_align256((size_t)G * D * L.lpad * eb);
+  L.kv = off; off += ls_align256((size_t)G * L.n_pages * LS_ATT_STAGE_BYTES);
   L.pg = off; off += ls_align256((size_t)(batch + 1) * 4);
   L.tiles = off; off += ls_align256((size_t)(batch + 1) * 4);
   L.vexp = off; off += ls_align256((size_t)G * L.n_pages * 4);
@@ -729,15 +711,15 @@ AttnWs attn_ws(int64_t total_k, int batch, int G, int D, int eb, bool bias) {
 }
 
 template <int DT, bool BIAS>
-void launch_tile(dim3 grid, hipStream_t s, const void* q, int64_t q_rs, const void* k, int64_t k_rs,
-                 const uint16_t* vt, const AttnWs& L, const int32_t* vexp, const float* cb,
+void launch_tile(dim3 grid, hipStream_t s, const void* q, int64_t q_rs, const uint8_t* kv,
+                 const AttnWs& L, const int32_t* vexp, const float* cb,
                  const int32_t* tok,
                  const int32_t* cu_q, const int32_t* cu_k, const int32_t* pg,
                  const int32_t* tiles, int batch, int64_t total_q, int G, int gs,
                  const int32_t* topk_idx, int take, float scale_log2, int causal, void* out,
                  float* lse) {
   hipLaunchKernelGGL((ls_attn_tile_kernel<DT, BIAS>), grid, dim3(LS_ATT_THREADS), 0, s,
-                     (const uint16_t*)q, q_rs, (const uint16_t*)k, k_rs, vt, L.lpad, vexp, cb, tok,
+                     (const uint16_t*)q, q_rs, kv, L.lpad, vexp, cb, tok,
                      L.n_pages, cu_q, cu_k, pg, tiles, batch, total_q, G, gs, topk_idx, take,
                      scale_log2, causal, (uint16_t*)out, lse, (int)(grid.x / 8));
 }
@@ -775,14 +757,12 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
                  q_row_stride % 8 == 0 && k_row_stride % 8 == 0 && v_row_stride % 8 == 0,
              LS_ERR_UNSUPPORTED,
              "%s: tensors must be 16-byte aligned with row strides %% 8 == 0", who);
-  const AttnWs L = attn_ws(total_k, batch, num_kv_heads, head_dim, 2, bias);
-  LS_REQUIRE(L.lpad * 2 * head_dim < (1LL << 32) && 64LL * k_row_stride * 2 < (1LL << 31),
-             LS_ERR_UNSUPPORTED, "%s: too many keys for 32-bit copy offsets", who);
+  const AttnWs L = attn_ws(total_k, batch, num_kv_heads, bias);
   LS_REQUIRE(workspace && workspace_bytes >= L.total, LS_ERR_WORKSPACE,
              "%s: workspace needs %zu bytes", who, L.total);
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
-  uint16_t* vt = (uint16_t*)(ws + L.vt);
+  uint8_t* kv = (uint8_t*)(ws + L.kv);
   int32_t* pg = (int32_t*)(ws + L.pg);
   int32_t* vexp = (int32_t*)(ws + L.vexp);
   int32_t* tiles = (int32_t*)(ws + L.tiles);
@@ -795,12 +775,14 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   if (total_k > 0) {
     const dim3 vgrid((unsigned)((total_k + 63) / 64 + batch), num_kv_heads);
     if (dtype == LS_BF16)
-      hipLaunchKernelGGL((ls_vt_kernel<LS_BF16, 128>), vgrid, dim3(256), 0, s, (const uint16_t*)v,
-                         v_row_stride, cu_seqlens_k, pg, batch, L.lpad, L.n_pages, vt, vexp);
+      hipLaunchKernelGGL(ls_kv_stage_kernel<LS_BF16>, vgrid, dim3(256), 0, s, (const uint16_t*)k,
+                         k_row_stride, (const uint16_t*)v, v_row_stride, cu_seqlens_k, pg, batch,
+                         L.n_pages, kv, vexp);
     else
-      hipLaunchKernelGGL((ls_vt_kernel<LS_F16, 128>), vgrid, dim3(256), 0, s, (const uint16_t*)v,
-                         v_row_stride, cu_seqlens_k, pg, batch, L.lpad, L.n_pages, vt, vexp);
-    if ((rc = ls_check_launch("ls_vt_kernel"))) return rc;
+      hipLaunchKernelGGL(ls_kv_stage_kernel<LS_F16>, vgrid, dim3(256), 0, s, (const uint16_t*)k,
+                         k_row_stride, (const uint16_t*)v, v_row_stride, cu_seqlens_k, pg, batch,
+                         L.n_pages, kv, vexp);
+    if ((rc = ls_check_launch("ls_kv_stage_kernel"))) return rc;
     if (bias) {
       if (cis_dtype == LS_BF16)
         hipLaunchKernelGGL(ls_bias_kernel<LS_BF16>, vgrid, dim3(64), 0, s, (const uint16_t*)cis,
@@ -820,7 +802,7 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   const int64_t tile_bound = (total_q + LS_ATT_TILE - 1) / LS_ATT_TILE + batch;
   const dim3 grid((unsigned)(8 * ((tile_bound + 7) / 8)), num_kv_heads, (gs + 15) / 16);
 #define LS_TILE_ARGS                                                                              \
-  grid, s, q, q_row_stride, k, k_row_stride, vt, L, vexp, cb, tok, cu_seqlens_q, cu_seqlens_k, pg,\
+  grid, s, q, q_row_stride, kv, L, vexp, cb, tok, cu_seqlens_q, cu_seqlens_k, pg,              \
       tiles, batch, total_q, num_kv_heads, gs, topk_idx, take, scale_log2, causal, out, lse
   if (dtype == LS_BF16) {
     if (bias) launch_tile<LS_BF16, true>(LS_TILE_ARGS);
@@ -838,14 +820,18 @@ extern "C" size_t ls_sparse_attn_workspace_size(int64_t total_k, int32_t batch,
                                                 int32_t num_kv_heads, int32_t head_dim,
                                                 int32_t max_seqlen_k, int32_t dtype) {
   (void)max_seqlen_k;
-  return attn_ws(total_k, batch, num_kv_heads, head_dim, (int)ls_dtype_bytes(dtype), false).total;
+  (void)head_dim;
+  (void)dtype;
+  return attn_ws(total_k, batch, num_kv_heads, false).total;
 }
 
 extern "C" size_t ls_nosa_attn_workspace_size(int64_t total_k, int32_t batch,
                                               int32_t num_kv_heads, int32_t head_dim,
                                               int32_t max_seqlen_k, int32_t dtype) {
   (void)max_seqlen_k;
-  return attn_ws(total_k, batch, num_kv_heads, head_dim, (int)ls_dtype_bytes(dtype), true).total;
+  (void)head_dim;
+  (void)dtype;
+  return attn_ws(total_k, batch, num_kv_heads, true).total;
 }
 
 extern "C" int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const void* k,
