@@ -256,13 +256,13 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   __shared__ uint8_t s_uneed[LS_ATT_MAX_UNION];  // waves with a row on the page
   // Bit u of s_wneed[w] is set when a row of wave w selected union page u.
   __shared__ uint32_t s_wneed[LS_ATT_WAVES][LS_ATT_MAX_UNION / 32];
-  __shared__ int32_t s_sexp[LS_ATT_STAGES];  // V exponent of the page in each stage
   __shared__ int s_wsum[LS_ATT_WAVES];
   // Ring protocol: s_next = next union page to be claimed for copying;
-  // s_ready[st] = union index + 1 of the page whose copy into stage st has
-  // landed; s_done[st] = (union index << 8) | number of its waves done with
+  // s_rdy[st][0] = union index + 1 of the page whose copy into stage st has
+  // landed, s_rdy[st][1] = that page's V exponent (read together); s_done[st] = (union index << 8) | number of its waves done with
   // it, for the page in stage st (tagged, so a stale count never matches).
-  __shared__ uint32_t s_next, s_ready[LS_ATT_STAGES], s_done[LS_ATT_STAGES];
+  __shared__ uint32_t s_next, s_done[LS_ATT_STAGES];
+  __shared__ __align__(8) uint32_t s_rdy[LS_ATT_STAGES][2];
   __shared__ __align__(16) float s_bias[BIAS ? LS_ATT_STAGES * 64 : 4];
   static_assert(LS_ATT_TILE * LS_ATT_WORDS * 4 <= LS_ATT_STAGES * LS_ATT_STAGE_BYTES,
                 "page bitmaps must fit in the ring");
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   for (int i = tid; i < LS_ATT_WAVES * (LS_ATT_MAX_UNION / 32); i += LS_ATT_THREADS)
     s_wneed[i / (LS_ATT_MAX_UNION / 32)][i % (LS_ATT_MAX_UNION / 32)] = 0u;
   if (tid < LS_ATT_STAGES) {
-    s_ready[tid] = 0u;
+    s_rdy[tid][0] = 0u;
     s_done[tid] = 0u;
   }
   if (tid == 0) s_next = LS_ATT_STAGES;  // pages 0..3 are copied at the start
@@ -431,7 +431,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   // page it waits for) once every wave with rows on the stage's previous page
   // is done with it, issues its copy and goes back to waiting without
   // waiting for the copy: the copy's final load brings the page's token
-  // (union index + 1) from global memory into s_ready[stage], and a wave's
+  // (union index + 1) from global memory into s_rdy[stage][0], and a wave's
   // loads land in issue order, so the token lands after the page's K, V^T and
   // bias.  Computing waves never copy (the last wave on a page is often the
   // slowest one).  A page's copy depends only on earlier pages being
@@ -456,9 +456,9 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     // The page's V exponent, then last the ready token ui_copy + 1 (lane 0 only).
     if (lane == 0) {
       ls_dma4(vexp_seq + page, 0u,
-              (uint32_t)(uintptr_t)(ls_lds_void*)&s_sexp[ui_copy % LS_ATT_STAGES]);
+              (uint32_t)(uintptr_t)(ls_lds_void*)&s_rdy[ui_copy % LS_ATT_STAGES][1]);
       ls_dma4(tok + ui_copy + 1, 0u,
-              (uint32_t)(uintptr_t)(ls_lds_void*)&s_ready[ui_copy % LS_ATT_STAGES]);
+              (uint32_t)(uintptr_t)(ls_lds_void*)&s_rdy[ui_copy % LS_ATT_STAGES][0]);
     }
   };
   // Hands stage u % 4 to page u (its waves count from zero) and copies it.
@@ -491,14 +491,18 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     return true;
   };
   if (w < LS_ATT_STAGES && w < n_union) issue_copy(w);
-  auto is_ready = [&](int ui) {
-    return (uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
-               &s_ready[ui % LS_ATT_STAGES], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) ==
-           (uint32_t)ui + 1u;
+  // The ready token (low word) and V exponent (high word) of union page ui's
+  // stage, read in one access: the exponent lands before the token, so a
+  // read that sees the token sees the page's exponent.
+  auto stage_word = [&](int ui) -> uint64_t {
+    return __hip_atomic_load(reinterpret_cast<uint64_t*>(&s_rdy[ui % LS_ATT_STAGES][0]),
+                             __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+  auto is_ready = [&](int ui, uint64_t word) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)word) == (uint32_t)ui + 1u;
   };
 
-  auto compute_page = [&](int ui, int page, uint32_t sel) {
-    const int v_e = s_sexp[ui % LS_ATT_STAGES];
+  auto compute_page = [&](int ui, int page, uint32_t sel, int v_e) {
     const float p_unscale = __builtin_ldexpf(1.f, -v_e);
     const uint8_t* kb = s_ring + (ui % LS_ATT_STAGES) * LS_ATT_STAGE_BYTES;
     const uint8_t* vb = kb + LS_ATT_KBYTES;
@@ -623,19 +627,22 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   int ui = next_page(-1);
   uint32_t meta = ui < n_union ? s_umeta[ui] : 0u;
   while (ui < n_union) {
-    if (!is_ready(ui)) {
+    uint64_t sw = stage_word(ui);
+    if (!is_ready(ui, sw)) {
       // Bounded wait (the protocol cannot deadlock; the bound only guarantees
       // that a wave always finishes).
       for (int spin = 0; spin < (1 << 22); ++spin) {
         if (!try_claim(ui)) __builtin_amdgcn_s_sleep(1);
-        if (is_ready(ui)) break;
+        sw = stage_word(ui);
+        if (is_ready(ui, sw)) break;
       }
     }
 
     const int nxt = next_page(ui);
     const uint32_t meta_next = nxt < n_union ? s_umeta[nxt] : 0u;
     const uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)meta);
-    compute_page(ui, (int)(m >> 16), (m >> (LS_ATT_TPW * w)) & ROWS_MASK);
+    compute_page(ui, (int)(m >> 16), (m >> (LS_ATT_TPW * w)) & ROWS_MASK,
+                 __builtin_amdgcn_readfirstlane((int)(uint32_t)(sw >> 32)));
     // Done with the stage (the release orders this wave's reads of it first).
     if (lane == 0)
       __hip_atomic_fetch_add(&s_done[ui % LS_ATT_STAGES], 1u, __ATOMIC_RELEASE,
