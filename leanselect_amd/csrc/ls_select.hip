@@ -260,6 +260,11 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_mfma_kernel(
     const int32_t* __restrict__ blk_off, int batch, int64_t n_blk_launch, int init_blocks,
     int local_blocks, int64_t full_seq_len, uint16_t* __restrict__ out, int64_t out_stride) {
   constexpr int F = KS * 32;
+  // Each wave stages 16 steps of its scores (64 tokens x 64 pages) here and
+  // then writes whole 128-byte row segments; rows are padded to 68 halves so
+  // the per-step 16-bit writes of the sixteen token rows hit distinct banks.
+  constexpr int SP = 68;
+  __shared__ __align__(16) uint16_t s_out[4][64 * SP];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int g = blockIdx.y;
@@ -300,16 +305,47 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_mfma_kernel(
 
   // q~^T fragments (B operand) of the four 16-token column blocks.
   ls_u32x4 qf[4][KS];
-  bool tok_ok[4];
   int64_t tok[4];
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
-    tok_ok[tb] = tq0 + 16 * tb + r < tq_end;
     tok[tb] = min(tq0 + 16 * tb + r, tq_end - 1);
     const uint16_t* qrow = qt + ((int64_t)g * Nq + tok[tb]) * F + 8 * q;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[tb][ks] = ls_load16(qrow + 32 * ks);
   }
+
+  // Pages this wave writes, and whether 4-page pieces of a row may be stored
+  // as one 8-byte word.
+  const int pa = max(p_lo, 4 * jw_lo), pb = min(p_hi, 4 * jw_hi + 3);
+  const bool wide = (out_stride & 3) == 0 && ((uintptr_t)out & 7) == 0;
+  uint16_t* const so = s_out[w];
+  // Writes the staged steps of batch jb (pages 64 jb .. 64 jb + 63) that fall
+  // in [pa, pb] for the block's valid tokens: lane (token 4 it + lane / 16,
+  // piece lane % 16) stores pages 64 jb + 4 piece .. + 3.
+  auto flush = [&](int jb) {
+    const int pg0 = 64 * jb;
+    const int fa = max(pa, pg0), fb = min(pb, pg0 + 63);
+    if (fa > fb) return;
+    const int pc = lane & 15, pp = pg0 + 4 * pc;
+    const bool full = wide && pp >= fa && pp + 3 <= fb;
+    const bool part = !full && pp <= fb && pp + 3 >= fa;
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int tk = 4 * it + (lane >> 4);
+      if (tq0 + tk >= tq_end || !(full || part)) continue;
+      const uint2 v = *reinterpret_cast<const uint2*>(so + tk * SP + 4 * pc);
+      uint16_t* dst = out + ((int64_t)g * Nq + tq0 + tk) * out_stride + pp;
+      if (full) {
+        *reinterpret_cast<uint2*>(dst) = v;
+      } else {
+        const uint16_t h[4] = {(uint16_t)(v.x & 0xffffu), (uint16_t)(v.x >> 16),
+                               (uint16_t)(v.y & 0xffffu), (uint16_t)(v.y >> 16)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (pp + i >= fa && pp + i <= fb) dst[i] = h[i];
+      }
+    }
+  };
 
   const uint16_t* kbase = kt + ((int64_t)g * Na + a0) * F + 8 * q;
   float carry[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
@@ -324,9 +360,12 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_mfma_kernel(
   // register budget, one for the widest routers.
   constexpr int PD = KS <= 6 ? 2 : 1;
   // One 16-atom step on k~ fragments kc, prefetching the fragments of step
-  // j + PD into kn.
+  // j + PD into kn.  The prefetch is unconditional (load_k clamps its rows, so
+  // steps past the end reread the last atom): a branch around it would make
+  // the compiler's wait counting conservative, and every step would then wait
+  // for the stores of the previous ones.
   auto step = [&](int j, const ls_u32x4 (&kc)[KS], ls_u32x4 (&kn)[KS]) {
-    if (j + PD <= jw_hi) load_k(kn, j + PD);
+    load_k(kn, j + PD);
     ls_f32x4 acc[4];
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
@@ -335,8 +374,6 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_mfma_kernel(
       for (int ks = 0; ks < KS; ++ks) acc[tb] = LsElem<DT>::mfma(kc[ks], qf[tb][ks], acc[tb]);
     }
     const int atom0 = 16 * j + 4 * q;
-    const int p = 4 * j + q;
-    const bool write = j >= jw_lo && p >= p_lo && p <= p_hi;
     const bool tail = 16 * j + 15 >= n_at;  // uniform: only the last step has atoms past the end
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
@@ -349,16 +386,16 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_mfma_kernel(
       const float rot = ls_shfl(acc[tb][3], (lane - 16) & 63);
       const float prev = q == 0 ? carry[tb] : rot;
       carry[tb] = rot;
-      if (write && tok_ok[tb])
-        out[((int64_t)g * Nq + tok[tb]) * out_stride + p] = LsElem<DT>::from_f(fmaxf(m4, prev));
+      so[(16 * tb + r) * SP + 4 * (j & 15) + q] = LsElem<DT>::from_f(fmaxf(m4, prev));
     }
+    if ((j & 15) == 15 || j == jw_hi) flush(j >> 4);
   };
   // PD + 1 fragment buffers used in turn (no register copies between steps).
   int j = j_first;
   if constexpr (PD == 2) {
     ls_u32x4 kA[KS], kB[KS], kC[KS];
     load_k(kA, j_first);
-    if (j_first < jw_hi) load_k(kB, j_first + 1);
+    load_k(kB, j_first + 1);
     for (; j + 2 <= jw_hi; j += 3) {
       step(j, kA, kC);
       step(j + 1, kB, kA);
