@@ -120,6 +120,71 @@ __device__ __forceinline__ int ls_lanes_below(uint64_t mask) {
                                         __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
+// k-th largest key of one wave-wide row: keys live in NS register slots of
+// 64 lanes, 0 marks an empty slot and is never counted.  The result is the
+// largest T with #{key >= T} >= kk (0 when fewer than kk keys are nonzero).
+// Plain bisection over the bits below top_bit, starting from prefix T.
+template <int NS>
+__device__ __forceinline__ uint32_t ls_kth_bisect(const uint32_t (&key)[NS], int kk, uint32_t T,
+                                                  int top_bit) {
+#pragma unroll 1
+  for (int bit = top_bit; bit >= 0; --bit) {
+    const uint32_t cand = T | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) cnt += __popcll(__ballot(key[s] >= cand));
+    if (cnt >= kk) T = cand;
+  }
+  return T;
+}
+
+// The same for long rows (kk <= 128), with a wave-private LDS scratch of 256
+// words.  lo = the kk-th largest of the lanes' two largest keys is a lower
+// bound of the answer (those keys are a subset of the row), so every key the
+// answer counts is >= lo; the keys >= lo are gathered into four slots (when
+// at most 256 of them) and bisected from the common bit prefix of lo and the
+// row maximum, which the answer shares.  Otherwise plain bisection.
+template <int NS, int BITS>
+__device__ __forceinline__ uint32_t ls_kth_key_row(const uint32_t (&key)[NS], int kk,
+                                                   uint32_t* __restrict__ scr, int lane) {
+  if constexpr (NS <= 4) {
+    return ls_kth_bisect<NS>(key, kk, 0u, BITS - 1);
+  } else {
+    if (kk < 1 || kk > 128) return ls_kth_bisect<NS>(key, kk, 0u, BITS - 1);
+    uint32_t m1 = 0u, m2 = 0u;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      m2 = max(m2, min(m1, key[s]));
+      m1 = max(m1, key[s]);
+    }
+    const uint32_t mm[2] = {m1, m2};
+    const uint32_t lo = ls_kth_bisect<2>(mm, kk, 0u, BITS - 1);
+    if (lo == 0u) return ls_kth_bisect<NS>(key, kk, 0u, BITS - 1);
+    int n = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const bool sv = key[s] >= lo;
+      const uint64_t mk = __ballot(sv);
+      const int pos = n + ls_lanes_below(mk);
+      if (sv && pos < 256) scr[pos] = key[s];
+      n += __popcll(mk);
+    }
+    if (n > 256) return ls_kth_bisect<NS>(key, kk, 0u, BITS - 1);
+    uint32_t sk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sk[i] = i * 64 + lane < n ? scr[i * 64 + lane] : 0u;
+    uint32_t hi = m1;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, LS_WAVE));
+    hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)hi);
+    const uint32_t d = lo ^ hi;
+    if (d == 0u) return lo;
+    const int tb = 31 - __builtin_clz(d);
+    const uint32_t T0 = tb >= 31 ? 0u : (lo & ~((2u << tb) - 1u));
+    return ls_kth_bisect<4>(sk, kk, T0, tb);
+  }
+}
+
 // Index of the segment containing `x` in a nondecreasing prefix array
 // `off[0..n]` (off[0] == 0): largest b < n with off[b] <= x.
 __device__ __forceinline__ int ls_find_segment(const int32_t* off, int n, int64_t x) {

@@ -227,20 +227,6 @@ int ls_nosa_cis_pages_launch(const void* cis, int64_t cis_rs, int cis_dtype, con
 // ---------------------------------------------------------------------------
 // Threshold T such that #{key > T} < kk <= #{key >= T} (bisection over the
 // key bits with ballot counts; keys of inactive lanes are 0).
-template <int NS, int BITS>
-__device__ __forceinline__ uint32_t ls_kth_key(const uint32_t (&key)[NS], int kk) {
-  uint32_t T = 0;
-#pragma unroll 1
-  for (int bit = BITS - 1; bit >= 0; --bit) {
-    const uint32_t cand = T | (1u << bit);
-    int cnt = 0;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) cnt += __popcll(__ballot(key[s] >= cand));
-    if (cnt >= kk) T = cand;
-  }
-  return T;
-}
-
 // Marks the kk largest keys (ties to the lower page) in sel (bit s of the lane).
 template <int NS>
 __device__ __forceinline__ void ls_mark_topk(const uint32_t (&key)[NS], uint32_t T, int kk,
@@ -268,7 +254,8 @@ template <int NS, bool KEY32, bool CIS32>
 __device__ __forceinline__ void ls_nosa_topk_row(
     const void* __restrict__ P, int64_t prow, const float* __restrict__ cpg_seq, int n_scored,
     int out_len, int off_bq, int q_idx, int init_blocks, int local_blocks, int qk_select,
-    int take, uint32_t pinf1, uint32_t ninf1, int lane, int32_t* __restrict__ orow) {
+    int take, uint32_t pinf1, uint32_t ninf1, int lane, int32_t* __restrict__ orow,
+    uint32_t* __restrict__ scr) {
   constexpr int NW = (NS + 31) / 32;
   // Every +inf (forced or shortlisted) and every -inf is one key, so ties among
   // them go to the lower page as in a stable sort.  Stage 1 keys come from the
@@ -301,7 +288,8 @@ __device__ __forceinline__ void ls_nosa_topk_row(
   uint32_t shortlist[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) shortlist[i] = 0u;
-  ls_mark_topk<NS>(key, ls_kth_key<NS, KEY32 ? 32 : 16>(key, qk_select), qk_select, shortlist);
+  ls_mark_topk<NS>(key, ls_kth_key_row<NS, KEY32 ? 32 : 16>(key, qk_select, scr, lane), qk_select,
+                   shortlist);
   // Stage 2 keys.
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
@@ -320,7 +308,7 @@ __device__ __forceinline__ void ls_nosa_topk_row(
   uint32_t chosen[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) chosen[i] = 0u;
-  ls_mark_topk<NS>(key, ls_kth_key<NS, CIS32 ? 32 : 16>(key, take), take, chosen);
+  ls_mark_topk<NS>(key, ls_kth_key_row<NS, CIS32 ? 32 : 16>(key, take, scr, lane), take, chosen);
   // Emission: chosen pages <= q_idx in ascending order, then -1.
   int out_pos = 0;
 #pragma unroll
@@ -328,7 +316,8 @@ __device__ __forceinline__ void ls_nosa_topk_row(
     const int p = s * 64 + lane;
     const bool emit = ((chosen[s >> 5] >> (s & 31)) & 1u) && p <= q_idx;
     const uint64_t m = __ballot(emit);
-    if (emit) orow[out_pos + ls_lanes_below(m)] = p;
+    const int pos = out_pos + ls_lanes_below(m);
+    if (emit && pos < take) orow[pos] = p;  // at most take by construction
     out_pos += __popcll(m);
   }
   for (int i = out_pos + lane; i < take; i += 64) orow[i] = -1;
@@ -341,9 +330,12 @@ __global__ __launch_bounds__(256) void ls_nosa_topk_kernel(
     const int32_t* __restrict__ cu_a, int batch, int64_t total_q, int G, int max_seqlen_q,
     int out_len, int init_blocks, int local_blocks, int qk_select, int take, int block_size,
     uint32_t pinf1, uint32_t ninf1, int32_t* __restrict__ topk_idx) {
+  __shared__ uint32_t s_scr[4][256];  // per-wave gather space of the k-th key search
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + wv;
   if (row >= (int64_t)G * total_q) return;
+  uint32_t* const scr = s_scr[wv];
   const int g = (int)(row / total_q);
   const int64_t t = row - (int64_t)g * total_q;
   const int b = ls_find_segment(cu_q, batch, t);
@@ -358,14 +350,14 @@ __global__ __launch_bounds__(256) void ls_nosa_topk_kernel(
   int32_t* orow = topk_idx + row * take;
   const int64_t prow = row * p_stride;
   const int n_slots = (out_len + 63) >> 6;
-  if (n_slots <= 1) return ls_nosa_topk_row<1, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 2) return ls_nosa_topk_row<2, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 4 || KPL <= 4) return ls_nosa_topk_row<(KPL < 4 ? KPL : 4), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 8 || KPL <= 8) return ls_nosa_topk_row<(KPL < 8 ? KPL : 8), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 16 || KPL <= 16) return ls_nosa_topk_row<(KPL < 16 ? KPL : 16), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 32 || KPL <= 32) return ls_nosa_topk_row<(KPL < 32 ? KPL : 32), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  if (n_slots <= 64 || KPL <= 64) return ls_nosa_topk_row<(KPL < 64 ? KPL : 64), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
-  return ls_nosa_topk_row<KPL, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow);
+  if (n_slots <= 1) return ls_nosa_topk_row<1, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
+  if (n_slots <= 2) return ls_nosa_topk_row<2, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
+  if (n_slots <= 4 || KPL <= 4) return ls_nosa_topk_row<(KPL < 4 ? KPL : 4), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
+  if (n_slots <= 8 || KPL <= 8) return ls_nosa_topk_row<(KPL < 8 ? KPL : 8), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
+  if (n_slots <= 16 || KPL <= 16) return ls_nosa_topk_row<(KPL < 16 ? KPL : 16), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
+  if (n_slots <= 32 || KPL <= 32) return ls_nosa_topk_row<(KPL < 32 ? KPL : 32), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
+  if (n_slots <= 64 || KPL <= 64) return ls_nosa_topk_row<(KPL < 64 ? KPL : 64), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
+  return ls_nosa_topk_row<KPL, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
 }
 
 template <bool KEY32, bool CIS32>

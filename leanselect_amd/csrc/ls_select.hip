@@ -475,7 +475,8 @@ __global__ __launch_bounds__(256) void ls_score_f32_kernel(
 template <int NS, bool KEY32>
 __device__ __forceinline__ void ls_topk_row(const void* __restrict__ P, int64_t base, int cn,
                                             int kk, int lo_end, int lane,
-                                            int32_t* __restrict__ orow) {
+                                            int32_t* __restrict__ orow,
+                                            uint32_t* __restrict__ scr) {
   uint32_t key[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
@@ -490,15 +491,7 @@ __device__ __forceinline__ void ls_topk_row(const void* __restrict__ P, int64_t 
     else k = ls_order_key16((uint16_t)key[s]);
     key[s] = s * 64 + lane < cn ? k : 0u;
   }
-  uint32_t T = 0;
-#pragma unroll 1
-  for (int bit = KEY32 ? 31 : 15; bit >= 0; --bit) {
-    const uint32_t cand = T | (1u << bit);
-    int cnt = 0;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) cnt += __popcll(__ballot(key[s] >= cand));
-    if (cnt >= kk) T = cand;
-  }
+  const uint32_t T = ls_kth_key_row<NS, KEY32 ? 32 : 16>(key, kk, scr, lane);
   int gt = 0;
 #pragma unroll
   for (int s = 0; s < NS; ++s) gt += __popcll(__ballot(key[s] > T));
@@ -514,7 +507,8 @@ __device__ __forceinline__ void ls_topk_row(const void* __restrict__ P, int64_t 
     const int eq_rank = eq_before + ls_lanes_below(eq_mask);
     const bool sel = valid && (key[s] > T || (eq && eq_rank < m));
     const uint64_t sel_mask = __ballot(sel);
-    if (sel) orow[out_pos + ls_lanes_below(sel_mask)] = lo_end + c;
+    const int pos = out_pos + ls_lanes_below(sel_mask);
+    if (sel && pos < lo_end + kk) orow[pos] = lo_end + c;  // exactly kk by construction
     out_pos += __popcll(sel_mask);
     eq_before += __popcll(eq_mask);
   }
@@ -525,13 +519,16 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
     const void* __restrict__ P, int64_t p_stride, const int32_t* __restrict__ cu_q,
     const int32_t* __restrict__ cu_a, int batch, int64_t total_q, int G, int take,
     int init_blocks, int local_blocks, int block_size, int32_t* __restrict__ topk_idx) {
+  __shared__ uint32_t s_scr[4][256];  // per-wave gather space of the k-th key search
   const int lane = threadIdx.x & 63;
   // The wave index is uniform: keep the row and everything derived from it scalar.
-  const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + wv;
   if (row >= (int64_t)G * total_q) return;
   const int g = (int)(row / total_q);
   const int64_t t = row - (int64_t)g * total_q;
   int32_t* orow = topk_idx + row * take;
+  uint32_t* const scr = s_scr[wv];
   const int b = ls_find_segment(cu_q, batch, t);
   const int64_t tr = t - cu_q[b];
   const int lq = cu_q[b + 1] - cu_q[b];
@@ -563,14 +560,14 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
   // so the branch picks one straight-line body per wave.
   const int64_t base = row * p_stride + lo_end;
   const int n_slots = (cn + 63) >> 6;
-  if (n_slots <= 1) return ls_topk_row<1, KEY32>(P, base, cn, kk, lo_end, lane, orow);
-  if (n_slots <= 2) return ls_topk_row<2, KEY32>(P, base, cn, kk, lo_end, lane, orow);
-  if (n_slots <= 4 || KPL <= 4) return ls_topk_row<(KPL < 4 ? KPL : 4), KEY32>(P, base, cn, kk, lo_end, lane, orow);
-  if (n_slots <= 8 || KPL <= 8) return ls_topk_row<(KPL < 8 ? KPL : 8), KEY32>(P, base, cn, kk, lo_end, lane, orow);
-  if (n_slots <= 16 || KPL <= 16) return ls_topk_row<(KPL < 16 ? KPL : 16), KEY32>(P, base, cn, kk, lo_end, lane, orow);
-  if (n_slots <= 32 || KPL <= 32) return ls_topk_row<(KPL < 32 ? KPL : 32), KEY32>(P, base, cn, kk, lo_end, lane, orow);
-  if (n_slots <= 64 || KPL <= 64) return ls_topk_row<(KPL < 64 ? KPL : 64), KEY32>(P, base, cn, kk, lo_end, lane, orow);
-  return ls_topk_row<KPL, KEY32>(P, base, cn, kk, lo_end, lane, orow);
+  if (n_slots <= 1) return ls_topk_row<1, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+  if (n_slots <= 2) return ls_topk_row<2, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+  if (n_slots <= 4 || KPL <= 4) return ls_topk_row<(KPL < 4 ? KPL : 4), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+  if (n_slots <= 8 || KPL <= 8) return ls_topk_row<(KPL < 8 ? KPL : 8), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+  if (n_slots <= 16 || KPL <= 16) return ls_topk_row<(KPL < 16 ? KPL : 16), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+  if (n_slots <= 32 || KPL <= 32) return ls_topk_row<(KPL < 32 ? KPL : 32), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+  if (n_slots <= 64 || KPL <= 64) return ls_topk_row<(KPL < 64 ? KPL : 64), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+  return ls_topk_row<KPL, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
 }
 
 // ---------------------------------------------------------------------------
