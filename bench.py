@@ -259,7 +259,7 @@ def main() -> None:
                       "sparse_attention": round(ms_attn, 4)},
         "roofline": {
             "kernel": ("ls_attn_tile_kernel (block-sparse attention"
-                       + (", CIS key bias" if nosa else "") + "; timed with its V staging and plan kernels)"),
+                       + (", CIS key bias" if nosa else "") + "; timed with its K/V staging and plan kernels)"),
             "bound": "mfma",
             "achieved": round(attn_tflops, 2),
             "peak": BF16_PEAK_TFLOPS,
