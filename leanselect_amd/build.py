@@ -37,7 +37,7 @@ FILE_FLAGS = {
     "ls_attention": ["-mno-amdgpu-ieee", "-fno-honor-nans"],
     # MFMAs accumulate in ordinary VGPRs, so their results need no copies out
     # of the accumulation registers before the pooling reads them.
-    "ls_select": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "ls_select": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mno-amdgpu-ieee", "-fno-honor-nans"],
 }
 
 

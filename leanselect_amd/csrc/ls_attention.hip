@@ -98,7 +98,6 @@ __global__ void ls_attn_plan_kernel(const int32_t* __restrict__ cu_q,
 #define LS_ATT_WORDS (LS_ATTN_MAX_PAGES / 32)
 #define LS_ATT_MAX_UNION (LS_ATT_TILE * LS_ATTN_MAX_TAKE)
 
-typedef __attribute__((address_space(3))) void ls_lds_void;
 typedef _Float16 ls_half2 __attribute__((ext_vector_type(2)));
 typedef float ls_float2 __attribute__((ext_vector_type(2)));
 
@@ -183,39 +182,8 @@ __global__ __launch_bounds__(256) void ls_kv_stage_kernel(
   }
 }
 
-// One 16-byte global->LDS load per lane from sbase + voff bytes (lane l lands
-// at lds_off + 16 l; sbase and lds_off are wave-uniform, voff a 32-bit lane
-// offset).  Issued as inline asm so the compiler's wait insertion does not
-// treat every later LDS read as aliasing the in-flight copy (which would
-// drain the whole prefetch queue); the kernel orders the copies itself with
-// vmcnt waits and a barrier per page.  An SALU write of M0 followed by a
-// global load with LDS destination needs one wait state, which the compiler
-// cannot insert inside the asm block.
-__device__ __forceinline__ void ls_dma16(const void* sbase, uint32_t voff, uint32_t lds_off) {
-  const uint64_t a = (uint64_t)(uintptr_t)sbase;
-  // (readfirstlane returns int: widen each half as unsigned, or the low half
-  // would be sign-extended into the high one.)
-  const uint64_t sa = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
-                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(voff), "s"(sa), "s"((uint32_t)__builtin_amdgcn_readfirstlane(lds_off))
-               : "memory", "m0");
-}
 
-// One 4-byte global->LDS load per active lane (lane l lands at lds_off + 4 l).
-__device__ __forceinline__ void ls_dma4(const void* sbase, uint32_t voff, uint32_t lds_off) {
-  const uint64_t a = (uint64_t)(uintptr_t)sbase;
-  const uint64_t sa = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
-                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
-               :
-               : "v"(voff), "s"(sa), "s"((uint32_t)__builtin_amdgcn_readfirstlane(lds_off))
-               : "memory", "m0");
-}
 
-// lgkmcnt(0) with the other counters left alone (gfx9 encoding).
-#define LS_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(0xf | (0x7 << 4) | (0x3 << 14))
 
 // Two float32 -> one packed fp16 pair (round to nearest even).
 __device__ __forceinline__ uint32_t ls_pack_f16x2(float a, float b) {
@@ -229,9 +197,6 @@ __device__ __forceinline__ float ls_sum_f16x2(uint32_t x, float acc) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(ls_half2, x), one, acc, false);
 }
 
-// vmcnt(n) with the other counters left alone (gfx9 encoding).
-#define LS_WAIT_VMCNT(n) \
-  __builtin_amdgcn_s_waitcnt(((n) & 0xf) | (((n) >> 4) << 14) | (0x7 << 4) | (0xf << 8))
 
 // ---------------------------------------------------------------------------
 // Per-tile union plans, built by their own kernel before the tile kernel runs

@@ -185,6 +185,49 @@ __device__ __forceinline__ uint32_t ls_kth_key_row(const uint32_t (&key)[NS], in
   }
 }
 
+// ---------------------------------------------------------------------------
+// Direct global->LDS copies and counter waits (gfx9 encodings).
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void ls_lds_void;
+
+// One 16-byte global->LDS load per lane from sbase + voff bytes (lane l lands
+// at lds_off + 16 l; sbase and lds_off are wave-uniform, voff a 32-bit lane
+// offset).  Issued as inline asm so the compiler's wait insertion does not
+// treat every later LDS read as aliasing the in-flight copy (which would
+// drain the whole prefetch queue); callers order the copies themselves with
+// vmcnt waits and barriers or ready tokens.  An SALU write of M0 followed by a
+// global load with LDS destination needs one wait state, which the compiler
+// cannot insert inside the asm block.
+__device__ __forceinline__ void ls_dma16(const void* sbase, uint32_t voff, uint32_t lds_off) {
+  const uint64_t a = (uint64_t)(uintptr_t)sbase;
+  // (readfirstlane returns int: widen each half as unsigned, or the low half
+  // would be sign-extended into the high one.)
+  const uint64_t sa = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
+                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sa), "s"((uint32_t)__builtin_amdgcn_readfirstlane(lds_off))
+               : "memory", "m0");
+}
+
+// One 4-byte global->LDS load per active lane (lane l lands at lds_off + 4 l).
+__device__ __forceinline__ void ls_dma4(const void* sbase, uint32_t voff, uint32_t lds_off) {
+  const uint64_t a = (uint64_t)(uintptr_t)sbase;
+  const uint64_t sa = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
+                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :
+               : "v"(voff), "s"(sa), "s"((uint32_t)__builtin_amdgcn_readfirstlane(lds_off))
+               : "memory", "m0");
+}
+
+// lgkmcnt(0) with the other counters left alone (gfx9 encoding).
+#define LS_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(0xf | (0x7 << 4) | (0x3 << 14))
+
+// vmcnt(n) with the other counters left alone (gfx9 encoding).
+#define LS_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 0xf) | (((n) >> 4) << 14) | (0x7 << 4) | (0xf << 8))
+
 // Index of the segment containing `x` in a nondecreasing prefix array
 // `off[0..n]` (off[0] == 0): largest b < n with off[b] <= x.
 __device__ __forceinline__ int ls_find_segment(const int32_t* off, int n, int64_t x) {

@@ -223,12 +223,19 @@ __global__ __launch_bounds__(256) void ls_proj_f32_kernel(
 __global__ void ls_select_plan_kernel(const int32_t* __restrict__ cu_q, int batch, int bs,
                                       int32_t* __restrict__ blk_off) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int32_t acc = 0;
+  // blk_off[0..batch]: query blocks before each sequence; then sb_off[0..batch]
+  // (at blk_off + batch + 1): groups of four query blocks before each sequence.
+  int32_t* sb_off = blk_off + batch + 1;
+  int32_t acc = 0, acc4 = 0;
   blk_off[0] = 0;
+  sb_off[0] = 0;
   for (int b = 0; b < batch; ++b) {
     const int len = cu_q[b + 1] - cu_q[b];
-    acc += len > 0 ? (len + bs - 1) / bs : 0;
+    const int nb = len > 0 ? (len + bs - 1) / bs : 0;
+    acc += nb;
+    acc4 += (nb + 3) / 4;
     blk_off[b + 1] = acc;
+    sb_off[b + 1] = acc4;
   }
 }
 
@@ -414,6 +421,176 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_mfma_kernel(
   }
 }
 
+// Page scores on MFMA for router widths of 128 and 256 (KS 4 and 8), with the
+// k~ panel shared through LDS.  One workgroup = four consecutive 64-token query
+// blocks of one sequence and KV group, one per wave; all four walk the same
+// 16-atom steps (a wave past its own last page only keeps staging), so each
+// step's 16 k~ rows are read from global memory once per workgroup, by direct
+// global->LDS loads, two steps per batch, double buffered.  In LDS, 16-byte
+// chunk c of row R sits at position c ^ (R & 15), so the sixteen lanes of an
+// MFMA operand read hit distinct bank groups.  Scoring, the five-atom page max
+// and the staged row writes are those of ls_score_mfma_kernel, per wave.
+template <int DT, int KS, int MODE>
+__global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_panel_kernel(
+    const uint16_t* __restrict__ qt, int64_t Nq, const uint16_t* __restrict__ kt, int64_t Na,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_a,
+    const int32_t* __restrict__ sb_off, int batch, int64_t n_sb_launch, int init_blocks,
+    int local_blocks, int64_t full_seq_len, uint16_t* __restrict__ out, int64_t out_stride) {
+  static_assert(KS == 4 || KS == 8, "the chunk swizzle needs 16 or 32 chunks per row");
+  constexpr int F = KS * 32;
+  constexpr int ROWB = F * 2;          // bytes of one k~ row
+  constexpr int STEPB = 16 * ROWB;     // one 16-atom step
+  constexpr int NSTEP = 2;             // steps per staged batch
+  constexpr int BATCHB = NSTEP * STEPB;
+  constexpr int SP = 68;
+  __shared__ __align__(16) uint8_t s_k[2][BATCHB];
+  __shared__ __align__(16) uint16_t s_out[4][64 * SP];
+  __shared__ int s_jhi[4];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int g = blockIdx.y;
+
+  int64_t tq0, tq_end, a0, n_atoms;
+  int p_lo, p_hi;
+  if constexpr (MODE != LS_SCORE_FULL) {
+    const int64_t isb = n_sb_launch - 1 - (int64_t)blockIdx.x;  // longest rows first
+    if (isb >= sb_off[batch]) return;
+    const int b = ls_find_segment(sb_off, batch, isb);
+    const int qb = 4 * (int)(isb - sb_off[b]) + w;
+    tq0 = (int64_t)cu_q[b] + (int64_t)64 * qb;
+    tq_end = min(tq0 + 64, (int64_t)cu_q[b + 1]);
+    a0 = cu_a[b];
+    n_atoms = (int64_t)cu_a[b + 1] - a0;
+    if constexpr (MODE == LS_SCORE_SELECT) {
+      p_lo = init_blocks;
+      p_hi = qb - local_blocks - 1;
+    } else {  // full_seq_len carries the page-column count in this mode
+      p_lo = 0;
+      p_hi = (int)min(n_atoms / 4, full_seq_len - 1);
+    }
+  } else {
+    tq0 = 64LL * (4LL * blockIdx.x + w);
+    tq_end = min(tq0 + 64, Nq);
+    a0 = 0;
+    n_atoms = Na;
+    p_lo = 0;
+    p_hi = (int)((full_seq_len + 63) / 64) - 1;
+  }
+  // p_lo, a0 and n_atoms are the same for the four waves.
+  const bool active = tq0 < tq_end && n_atoms > 0 && p_lo <= p_hi;
+  const int jw_hi = active ? (p_hi >> 2) : -1;
+  if (lane == 0) s_jhi[w] = jw_hi;
+  __syncthreads();
+  const int j_hi = max(max(s_jhi[0], s_jhi[1]), max(s_jhi[2], s_jhi[3]));
+  if (j_hi < 0) return;  // no wave has a page to score (uniform)
+  const int j_lo = p_lo >> 2;
+  const int j_first = j_lo > 0 ? j_lo - 1 : 0;  // one step early primes the carry
+  const int n_at = (int)n_atoms;
+
+  // q~^T fragments (B operand) of the wave's four 16-token column blocks.
+  ls_u32x4 qf[4][KS];
+  int64_t tok[4];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    tok[tb] = active ? min(tq0 + 16 * tb + r, tq_end - 1) : 0;
+    const uint16_t* qrow = qt + ((int64_t)g * Nq + tok[tb]) * F + 8 * q;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[tb][ks] = active ? ls_load16(qrow + 32 * ks) : ls_u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // Staged score rows, written as whole 128-byte segments (see ls_score_mfma_kernel).
+  const int pa = p_lo, pb = p_hi;
+  const bool wide = (out_stride & 3) == 0 && ((uintptr_t)out & 7) == 0;
+  uint16_t* const so = s_out[w];
+  auto flush = [&](int jb) {
+    const int pg0 = 64 * jb;
+    const int fa = max(pa, pg0), fb = min(pb, pg0 + 63);
+    if (fa > fb) return;
+    const int pc = lane & 15, pp = pg0 + 4 * pc;
+    const bool full = wide && pp >= fa && pp + 3 <= fb;
+    const bool part = !full && pp <= fb && pp + 3 >= fa;
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int tk = 4 * it + (lane >> 4);
+      if (tq0 + tk >= tq_end || !(full || part)) continue;
+      const uint2 v = *reinterpret_cast<const uint2*>(so + tk * SP + 4 * pc);
+      uint16_t* dst = out + ((int64_t)g * Nq + tq0 + tk) * out_stride + pp;
+      if (full) {
+        *reinterpret_cast<uint2*>(dst) = v;
+      } else {
+        const uint16_t h[4] = {(uint16_t)(v.x & 0xffffu), (uint16_t)(v.x >> 16),
+                               (uint16_t)(v.y & 0xffffu), (uint16_t)(v.y >> 16)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (pp + i >= fa && pp + i <= fb) dst[i] = h[i];
+      }
+    }
+  };
+
+  // Batch of steps jb .. jb + NSTEP - 1 into buffer buf: 1 KB per load, lane l
+  // of load i covering batch bytes 1024 i + 16 l (row R, position c), from
+  // logical chunk c ^ (R & 15) of atom 16 jb + R (clamped to the last atom).
+  const uint8_t* kg = reinterpret_cast<const uint8_t*>(kt + ((int64_t)g * Na + a0) * F);
+  const uint32_t sk0 = (uint32_t)(uintptr_t)(ls_lds_void*)&s_k[0][0];
+  auto stage = [&](int jb, int buf) {
+#pragma unroll
+    for (int i = w; i < BATCHB / 1024; i += 4) {
+      const int byte = 1024 * i + 16 * lane;
+      const int row = byte / ROWB, pos = (byte % ROWB) / 16;
+      const int atom = min(16 * jb + row, n_at - 1);
+      const int chunk = pos ^ (row & 15);
+      ls_dma16(kg, (uint32_t)(atom * ROWB + 16 * chunk), sk0 + (uint32_t)(buf * BATCHB + 1024 * i));
+    }
+  };
+
+  float carry[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  auto step = [&](int j, const uint8_t* kb) {
+    ls_u32x4 kf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kf[ks] = *reinterpret_cast<const ls_u32x4*>(kb + r * ROWB + 16 * ((4 * ks + q) ^ r));
+    ls_f32x4 acc[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      acc[tb] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) acc[tb] = LsElem<DT>::mfma(kf[ks], qf[tb][ks], acc[tb]);
+    }
+    const int atom0 = 16 * j + 4 * q;
+    const bool tail = 16 * j + 15 >= n_at;  // uniform: only the last step has atoms past the end
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      if (tail) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (atom0 + i >= n_at) acc[tb][i] = -INFINITY;
+      }
+      const float m4 = fmaxf(fmaxf(acc[tb][0], acc[tb][1]), fmaxf(acc[tb][2], acc[tb][3]));
+      const float rot = ls_shfl(acc[tb][3], (lane - 16) & 63);
+      const float prev = q == 0 ? carry[tb] : rot;
+      carry[tb] = rot;
+      so[(16 * tb + r) * SP + 4 * (j & 15) + q] = LsElem<DT>::from_f(fmaxf(m4, prev));
+    }
+    if ((j & 15) == 15 || j == jw_hi) flush(j >> 4);
+  };
+
+  stage(j_first, 0);
+  int buf = 0;
+  for (int jb = j_first; jb <= j_hi; jb += NSTEP, buf ^= 1) {
+    // This batch has landed (every wave waited for its own loads), and every
+    // wave is done with the other buffer, which the next batch may overwrite.
+    LS_WAIT_VMCNT(0);
+    __syncthreads();
+    if (jb + NSTEP <= j_hi) stage(jb + NSTEP, buf ^ 1);
+#pragma unroll
+    for (int st = 0; st < NSTEP; ++st) {
+      const int j = jb + st;
+      if (j <= jw_hi) step(j, &s_k[buf][st * STEPB]);
+    }
+  }
+}
+
 // float32 page scores on the vector ALU: one thread per (group, token, page).
 // General pooling stride s = block_size / kernel_stride.
 template <int MODE>
@@ -588,7 +765,7 @@ WsLayout ws_layout(int64_t total_q, int64_t total_atoms, int batch, int H, int G
   L.wk = off; off += ls_align256((size_t)G * D * F * eb);
   L.qt = off; off += ls_align256((size_t)G * total_q * F * eb);
   L.kt = off; off += ls_align256((size_t)G * total_atoms * F * eb);
-  L.blk = off; off += ls_align256((size_t)(batch + 1) * 4);
+  L.blk = off; off += ls_align256((size_t)(batch + 1) * 2 * 4);
   L.p_stride = ((int64_t)max_pages + 63) & ~(int64_t)63;
   L.p = off; off += ls_align256((size_t)G * total_q * L.p_stride * eb);
   L.total = off;
@@ -700,6 +877,21 @@ int launch_score16(int F, dim3 grid, hipStream_t s, const void* qt, int64_t Nq, 
   const uint16_t* qp = (const uint16_t*)qt;
   const uint16_t* kp = (const uint16_t*)kt;
   uint16_t* op = (uint16_t*)out;
+  if (F == 128 || F == 256) {
+    // Four query blocks per workgroup sharing the k~ panel through LDS.
+    const int32_t* sb = MODE != LS_SCORE_FULL ? blk + batch + 1 : nullptr;
+    const int64_t n_sb = MODE != LS_SCORE_FULL ? (Nq + 255) / 256 + batch : ((Nq + 63) / 64 + 3) / 4;
+    const dim3 pgrid((unsigned)n_sb, grid.y);
+    if (F == 128)
+      hipLaunchKernelGGL((ls_score_panel_kernel<DT, 4, MODE>), pgrid, dim3(256), 0, s, qp, Nq, kp,
+                         Na, cu_q, cu_a, sb, batch, n_sb, init_blocks, local_blocks, full_len, op,
+                         out_stride);
+    else
+      hipLaunchKernelGGL((ls_score_panel_kernel<DT, 8, MODE>), pgrid, dim3(256), 0, s, qp, Nq, kp,
+                         Na, cu_q, cu_a, sb, batch, n_sb, init_blocks, local_blocks, full_len, op,
+                         out_stride);
+    return ls_check_launch("ls_score_panel_kernel");
+  }
   switch (F / 32) {
 #define LS_SCORE_CASE(KSV)                                                                   \
   case KSV:                                                                                  \
