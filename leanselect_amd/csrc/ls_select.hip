@@ -426,7 +426,7 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_mfma_kernel(
 // blocks of one sequence and KV group, one per wave; all four walk the same
 // 16-atom steps (a wave past its own last page only keeps staging), so each
 // step's 16 k~ rows are read from global memory once per workgroup, by direct
-// global->LDS loads, two steps per batch, double buffered.  In LDS, 16-byte
+// global->LDS loads, four steps per batch, double buffered.  In LDS, 16-byte
 // chunk c of row R sits at position c ^ (R & 15), so the sixteen lanes of an
 // MFMA operand read hit distinct bank groups.  Scoring, the five-atom page max
 // and the staged row writes are those of ls_score_mfma_kernel, per wave.
@@ -440,7 +440,7 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_panel_kernel(
   constexpr int F = KS * 32;
   constexpr int ROWB = F * 2;          // bytes of one k~ row
   constexpr int STEPB = 16 * ROWB;     // one 16-atom step
-  constexpr int NSTEP = 2;             // steps per staged batch
+  constexpr int NSTEP = 4;             // steps per staged batch
   constexpr int BATCHB = NSTEP * STEPB;
   constexpr int SP = 68;
   __shared__ __align__(16) uint8_t s_k[2][BATCHB];
