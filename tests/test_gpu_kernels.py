@@ -103,7 +103,17 @@ def test_projections_match_oracle(dtype):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("n", [700, 64, 33])
 def test_score_pages_matches_oracle(dtype, n):
-    s = _selector()
+    _check_score_pages(_selector(), dtype, n)
+
+
+@pytest.mark.parametrize("router", [(8, 32), (2, 32), (1, 64)])
+@pytest.mark.parametrize("n", [1000, 300])
+def test_score_pages_router_widths(router, n):
+    # Router widths 256 (shared-panel kernel, 8 k-slices) and 64 (per-wave kernel).
+    _check_score_pages(_selector(R=router[0], RD=router[1]), torch.bfloat16, n)
+
+
+def _check_score_pages(s, dtype, n):
     torch.manual_seed(3)
     q = torch.randn(n, 32, 128).to(dtype)
     k = torch.randn(n, 2, 128).to(dtype)

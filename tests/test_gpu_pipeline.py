@@ -57,6 +57,18 @@ def test_select_hidden_space_4k(dtype):
     assert rep.exact_rows >= 0.97 * rep.rows
 
 
+@pytest.mark.parametrize("router", [(8, 32), (2, 32), (3, 32)])
+def test_select_router_widths(router):
+    # F = 256 takes the scoring kernel with the shared LDS panel at 8 k-slices;
+    # F = 64 and 96 take the per-wave kernel (the panel needs 16 or 32 chunks a row).
+    rh, rd = router
+    case = workloads.hidden_space_layer((4096,), device=DEV, dtype=torch.bfloat16, seed=2,
+                                        router_heads=rh, router_dim=rd)
+    _, _, ids, rep = _check_select(case)
+    assert ids.shape == (2, 4096, 64)
+    assert rep.exact_rows >= 0.97 * rep.rows
+
+
 def test_select_ragged_with_short_sequences():
     lens = (8, 31, 32, 100, 1000, 2113, 64, 0, 4500)
     case = workloads.hidden_space_layer(lens, device=DEV, seed=2)
