@@ -165,12 +165,10 @@ int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t total_q, cons
                       int32_t take, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Workspace bytes needed by ls_sparse_attn_varlen for total_q query rows with
- * take ids each (the per-tile page plans grow with both) and total_k keys.
+ * Workspace bytes needed by ls_sparse_attn_varlen.
  */
-size_t ls_sparse_attn_workspace_size(int64_t total_q, int64_t total_k, int32_t batch,
-                                     int32_t num_kv_heads, int32_t head_dim,
-                                     int32_t max_seqlen_k, int32_t take, int32_t dtype);
+size_t ls_sparse_attn_workspace_size(int64_t total_k, int32_t batch, int32_t num_kv_heads,
+                                     int32_t head_dim, int32_t max_seqlen_k, int32_t dtype);
 
 /*
  * Block-sparse attention over per-token page plans:
@@ -271,12 +269,10 @@ int ls_nosa_select_prefill(const void* q, int64_t q_row_stride, int64_t total_q,
                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Workspace bytes needed by ls_nosa_attn_varlen (arguments as for
- * ls_sparse_attn_workspace_size).
+ * Workspace bytes needed by ls_nosa_attn_varlen.
  */
-size_t ls_nosa_attn_workspace_size(int64_t total_q, int64_t total_k, int32_t batch,
-                                   int32_t num_kv_heads, int32_t head_dim,
-                                   int32_t max_seqlen_k, int32_t take, int32_t dtype);
+size_t ls_nosa_attn_workspace_size(int64_t total_k, int32_t batch, int32_t num_kv_heads,
+                                   int32_t head_dim, int32_t max_seqlen_k, int32_t dtype);
 
 /*
  * NOSA attention: ls_sparse_attn_varlen (causal) with a per-key bias,

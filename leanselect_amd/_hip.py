@@ -40,7 +40,7 @@ SIGNATURES = {
     "ls_select_prefill": (
         _i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p,
                _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i32, _p, _sz, _p]),
-    "ls_sparse_attn_workspace_size": (_sz, [_i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "ls_sparse_attn_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32]),
     "ls_sparse_attn_varlen": (
         _i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _i32, _i64, _i64, _i32, _i32, _i32, _i32,
                _i32, _i32, _p, _i32, _i32, _f32, _i32, _p, _p, _p, _sz, _p]),
@@ -55,7 +55,7 @@ SIGNATURES = {
         _i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _p, _i32, _i32, _i32,
                _i32, _i32, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                _p, _i32, _p, _sz, _p]),
-    "ls_nosa_attn_workspace_size": (_sz, [_i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "ls_nosa_attn_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32]),
     "ls_nosa_attn_varlen": (
         _i32, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32, _p, _p, _i32, _i64, _i64, _i32,
                _i32, _i32, _i32, _i32, _i32, _p, _i32, _i32, _f32, _p, _p, _p, _sz, _p]),

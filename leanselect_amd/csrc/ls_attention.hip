@@ -198,149 +198,6 @@ __device__ __forceinline__ float ls_sum_f16x2(uint32_t x, float acc) {
 }
 
 
-// ---------------------------------------------------------------------------
-// Per-tile union plans, built by their own kernel before the tile kernel runs
-// (so a tile workgroup starts streaming after loading ~3 KB instead of
-// building its plan).  Slot of (group g, tile), ls_plan_layout(take) bytes:
-//   [0]      n_union (int32);
-//   [wneed]  LS_ATT_WAVES x wn words: bit u % 32 of word u / 32 of wave w is
-//            set when a row of wave w selected union page u;
-//   [umeta]  maxu words: page << 16 | mask of the tile rows that selected it,
-//            in visiting order;
-//   [uneed]  maxu bytes: the number of waves with a row on the page.
-// ---------------------------------------------------------------------------
-struct LsPlanLayout {
-  int maxu, wn;
-  int64_t wneed, umeta, uneed, bytes;
-};
-__host__ __device__ inline LsPlanLayout ls_plan_layout(int take) {
-  LsPlanLayout P;
-  P.maxu = LS_ATT_TILE * (take > 0 ? take : 0);
-  P.wn = (P.maxu + 31) / 32;
-  P.wneed = 16;
-  P.umeta = P.wneed + (int64_t)LS_ATT_WAVES * P.wn * 4;
-  P.uneed = P.umeta + (int64_t)P.maxu * 4;
-  P.bytes = (P.uneed + P.maxu + 255) & ~(int64_t)255;
-  return P;
-}
-
-#define LS_PLAN_THREADS 256
-// One workgroup per (tile, group): the tile rows' page plans are OR-ed into
-// LDS bitmaps (ids past a row's causal frontier, duplicates and -1 dropped),
-// and their union is laid out in a strided order: ascending page i goes to
-// slot i * stride mod n_union, a bijection for stride coprime to n_union.
-// Neighbouring pages tend to be selected by the same rows, and spreading them
-// out evens the work of the tile's waves over any window of pages.  (Empty or
-// one-page lists keep stride 1; a coprime odd stride below 64 + 7 exists for
-// any list accepted here, the loop bound only caps it.)
-__global__ __launch_bounds__(LS_PLAN_THREADS) void ls_attn_union_kernel(
-    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
-    const int32_t* __restrict__ tile_off, int batch, int64_t total_q,
-    const int32_t* __restrict__ topk_idx, int take, int causal, uint8_t* __restrict__ plan,
-    int64_t n_tiles_ws) {
-  constexpr uint32_t ROWS_MASK = LS_ATT_TPW == 32 ? 0xffffffffu : ((1u << LS_ATT_TPW) - 1u);
-  constexpr int PW = LS_PLAN_THREADS / 64;
-  __shared__ uint32_t s_bits[LS_ATT_TILE][LS_ATT_WORDS];
-  __shared__ uint32_t s_wneed[LS_ATT_WAVES][64];
-  __shared__ int s_wsum[PW];
-  static_assert(LS_ATT_WORDS <= LS_PLAN_THREADS, "one bitmap word per thread");
-  static_assert(LS_ATT_MAX_UNION <= 64 * 32, "at most 64 need words per wave");
-  const int tid = LS_TID;
-  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t tile = LS_BID_X;
-  if (tile >= tile_off[batch]) return;
-  const int g = LS_BID_Y;
-  const LsPlanLayout P = ls_plan_layout(take);
-  uint8_t* slot = plan + ((int64_t)g * n_tiles_ws + tile) * P.bytes;
-  uint32_t* umeta = reinterpret_cast<uint32_t*>(slot + P.umeta);
-  uint8_t* uneed = slot + P.uneed;
-
-  const int b = ls_find_segment(tile_off, batch, tile);
-  const int64_t t0 = (int64_t)cu_q[b] + LS_ATT_TILE * (tile - tile_off[b]);
-  const int n_rows = (int)min((int64_t)LS_ATT_TILE, (int64_t)cu_q[b + 1] - t0);
-  const int lq = cu_q[b + 1] - cu_q[b];
-  const int lk = cu_k[b + 1] - cu_k[b];
-  const int64_t tr0 = t0 - cu_q[b];
-  auto row_jmax = [&](int i) -> int64_t {
-    int64_t jm = lk - 1;
-    if (causal) jm = min(jm, tr0 + i + (int64_t)(lk - lq));
-    return jm;
-  };
-  const int64_t tile_jmax = row_jmax(n_rows - 1);
-  const int last_page =
-      tile_jmax >= 0 ? (int)min(tile_jmax / 64, (int64_t)LS_ATTN_MAX_PAGES - 1) : -1;
-  const int nwords = last_page / 32 + 1;
-
-  for (int i = tid; i < LS_ATT_TILE * nwords; i += LS_PLAN_THREADS) s_bits[i / nwords][i % nwords] = 0u;
-  for (int i = tid; i < LS_ATT_WAVES * 64; i += LS_PLAN_THREADS) s_wneed[i / 64][i % 64] = 0u;
-  __syncthreads();
-  if (last_page >= 0) {
-    const int32_t* ids = topk_idx + ((int64_t)g * total_q + t0) * take;
-    for (int i = tid; i < n_rows * take; i += LS_PLAN_THREADS) {
-      const int row = i / take;
-      const int p = ids[i];
-      const int64_t jm = row_jmax(row);
-      if (p >= 0 && jm >= 0 && p <= jm / 64 && p <= last_page)
-        atomicOr(&s_bits[row][p >> 5], 1u << (p & 31));
-    }
-  }
-  __syncthreads();
-  uint32_t word = 0u, row_word[LS_ATT_TILE];
-#pragma unroll
-  for (int i = 0; i < LS_ATT_TILE; ++i) {
-    row_word[i] = tid < nwords ? s_bits[i][tid] : 0u;
-    word |= row_word[i];
-  }
-  int wtot;
-  const int wpos = ls_wave_excl_scan(__popc(word), lane, &wtot);
-  if (lane == 0) s_wsum[w] = wtot;
-  __syncthreads();
-  int pos = wpos;
-  for (int i = 0; i < w; ++i) pos += s_wsum[i];
-  int n_union = 0;
-#pragma unroll
-  for (int i = 0; i < PW; ++i) n_union += s_wsum[i];
-  int stride = 1;
-  if (n_union > 1) {
-    for (int cand = 7; cand < 71; cand += 2) {
-      int a = cand, m = n_union;
-      while (m) {
-        const int t = a % m;
-        a = m;
-        m = t;
-      }
-      if (a == 1) {
-        stride = cand;
-        break;
-      }
-    }
-  }
-  while (word) {
-    const int bit = __ffs(word) - 1;
-    word &= word - 1;
-    const int page = tid * 32 + bit;
-    uint32_t rows = 0u;
-#pragma unroll
-    for (int i = 0; i < LS_ATT_TILE; ++i) rows |= ((row_word[i] >> bit) & 1u) << i;
-    const int dst = (int)(((uint32_t)pos * (uint32_t)stride) % (uint32_t)n_union);
-    int n_waves = 0;
-#pragma unroll
-    for (int i = 0; i < LS_ATT_WAVES; ++i) {
-      if (((rows >> (LS_ATT_TPW * i)) & ROWS_MASK) != 0u) {
-        ++n_waves;
-        atomicOr(&s_wneed[i][dst >> 5], 1u << (dst & 31));
-      }
-    }
-    umeta[dst] = ((uint32_t)page << 16) | rows;
-    uneed[dst] = (uint8_t)n_waves;
-    ++pos;
-  }
-  __syncthreads();
-  uint32_t* wneed = reinterpret_cast<uint32_t*>(slot + P.wneed);
-  for (int i = tid; i < LS_ATT_WAVES * P.wn; i += LS_PLAN_THREADS) wneed[i] = s_wneed[i / P.wn][i % P.wn];
-  if (tid == 0) *reinterpret_cast<int32_t*>(slot) = n_union;
-}
-
 // BIAS adds a per-key score bias (the NOSA eviction score, pre-scaled to base
 // 2): weight_j = 2^(scale_log2 * q.k_j + cb_j).  cb[g][64 pg_off[b] + j] is
 // staged like V^T and copied with each page (256 B per stage).
@@ -351,16 +208,20 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     const int32_t* __restrict__ tok, int64_t n_pages_ws,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
     const int32_t* __restrict__ pg_off, const int32_t* __restrict__ tile_off, int batch,
-    int64_t total_q, int G, int gs, const uint8_t* __restrict__ plan, int64_t n_tiles_ws,
-    int take, float scale_log2, int causal, uint16_t* __restrict__ out,
-    float* __restrict__ lse, int per_xcd) {
+    int64_t total_q, int G, int gs, const int32_t* __restrict__ topk_idx, int take,
+    float scale_log2, int causal, uint16_t* __restrict__ out, float* __restrict__ lse,
+    int per_xcd) {
   constexpr int D = 128;
   constexpr uint32_t ROWS_MASK = LS_ATT_TPW == 32 ? 0xffffffffu : ((1u << LS_ATT_TPW) - 1u);
+  // The per-row page bitmaps are only needed before streaming starts and
+  // share their LDS with the ring.
   __shared__ __align__(16) uint8_t s_ring[LS_ATT_STAGES * LS_ATT_STAGE_BYTES];
-  // Union entry (from the tile's plan): page << 16 | mask of the tile rows that
-  // selected it, and the number of waves with a row on the page.
+  // Union entry: page << 16 | mask of the tile rows that selected it.
   __shared__ uint32_t s_umeta[LS_ATT_MAX_UNION];
-  __shared__ uint8_t s_uneed[LS_ATT_MAX_UNION];
+  __shared__ uint8_t s_uneed[LS_ATT_MAX_UNION];  // waves with a row on the page
+  // Bit u of s_wneed[w] is set when a row of wave w selected union page u.
+  __shared__ uint32_t s_wneed[LS_ATT_WAVES][LS_ATT_MAX_UNION / 32];
+  __shared__ int s_wsum[LS_ATT_WAVES];
   // Ring protocol: s_next = next union page to be claimed for copying;
   // s_rdy[st][0] = union index + 1 of the page whose copy into stage st has
   // landed, s_rdy[st][1] = that page's V exponent (read together); s_done[st] = (union index << 8) | number of its waves done with
@@ -368,7 +229,15 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   __shared__ uint32_t s_next, s_done[LS_ATT_STAGES];
   __shared__ __align__(8) uint32_t s_rdy[LS_ATT_STAGES][2];
   __shared__ __align__(16) float s_bias[BIAS ? LS_ATT_STAGES * 64 : 4];
+  static_assert(LS_ATT_TILE * LS_ATT_WORDS * 4 <= LS_ATT_STAGES * LS_ATT_STAGE_BYTES,
+                "page bitmaps must fit in the ring");
   static_assert(LS_ATT_TILE <= 32, "row masks are 32-bit");
+  static_assert(LS_ATT_WORDS <= LS_ATT_THREADS, "one bitmap word per thread");
+#ifdef LS_ATT_NO_ALIAS
+  __shared__ uint32_t s_bits[LS_ATT_TILE][LS_ATT_WORDS];
+#else
+  uint32_t(*s_bits)[LS_ATT_WORDS] = reinterpret_cast<uint32_t(*)[LS_ATT_WORDS]>(s_ring);
+#endif
 
   const int tid = LS_TID;
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -395,8 +264,13 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     if (causal) jm = min(jm, tr0 + i + (int64_t)(lk - lq));
     return jm;
   };
+  const int64_t tile_jmax = row_jmax(n_rows - 1);
+  const int last_page =
+      tile_jmax >= 0 ? (int)min(tile_jmax / 64, (int64_t)LS_ATTN_MAX_PAGES - 1) : -1;
+  const int nwords = last_page / 32 + 1;
+
   // ---- per-row state: Q^T fragments (B operand), softmax stats, O^T ----
-  // (the Q loads are issued first; they land while the plan is loaded)
+  // (the Q loads are issued first; they land while the page list is built)
   ls_u32x4 qf[LS_ATT_TPW][4];
   // m_run: running max in scaled base-2 units (score * scale_log2); thr: the
   // raw score above which a key would exceed m_run by more than 2^8.
@@ -420,30 +294,93 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[j][db] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  // ---- the tile's union plan ----
-  const LsPlanLayout P = ls_plan_layout(take);
-  const uint8_t* slot = plan + ((int64_t)g * n_tiles_ws + tile) * P.bytes;
-  const int n_union = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int32_t*>(slot));
-  const uint32_t* umeta_g = reinterpret_cast<const uint32_t*>(slot + P.umeta);
-  const uint8_t* uneed_g = slot + P.uneed;
-  for (int i = tid; i < n_union; i += LS_ATT_THREADS) {
-    s_umeta[i] = umeta_g[i];
-    s_uneed[i] = uneed_g[i];
-  }
-  // This wave's pages: bit b of lane l is set when one of its rows selected
-  // union page 32 l + b (the union holds at most 64 x 32 pages).
-  static_assert(LS_ATT_MAX_UNION <= 64 * 32, "one need word per lane");
-  const uint32_t wneed =
-      lane < P.wn ? reinterpret_cast<const uint32_t*>(slot + P.wneed)[w * P.wn + lane] : 0u;
+  // ---- per-row page bitmaps and their sorted union ----
+  for (int i = tid; i < LS_ATT_TILE * nwords; i += LS_ATT_THREADS) s_bits[i / nwords][i % nwords] = 0u;
+  for (int i = tid; i < LS_ATT_WAVES * (LS_ATT_MAX_UNION / 32); i += LS_ATT_THREADS)
+    s_wneed[i / (LS_ATT_MAX_UNION / 32)][i % (LS_ATT_MAX_UNION / 32)] = 0u;
   if (tid < LS_ATT_STAGES) {
     s_rdy[tid][0] = 0u;
     s_done[tid] = 0u;
   }
   if (tid == 0) s_next = LS_ATT_STAGES;  // pages 0..3 are copied at the start
+  __syncthreads();
+  if (last_page >= 0) {
+    const int32_t* ids = topk_idx + ((int64_t)g * total_q + t0) * take;
+    for (int i = tid; i < n_rows * take; i += LS_ATT_THREADS) {
+      const int row = i / take;
+      const int p = ids[i];
+      const int64_t jm = row_jmax(row);
+      if (p >= 0 && jm >= 0 && p <= jm / 64 && p <= last_page)
+        atomicOr(&s_bits[row][p >> 5], 1u << (p & 31));
+    }
+  }
+  __syncthreads();
+  uint32_t word = 0u, row_word[LS_ATT_TILE];
+#pragma unroll
+  for (int i = 0; i < LS_ATT_TILE; ++i) {
+    row_word[i] = tid < nwords ? s_bits[i][tid] : 0u;
+    word |= row_word[i];
+  }
+  int wtot;
+  const int wpos = ls_wave_excl_scan(__popc(word), lane, &wtot);
+  if (lane == 0) s_wsum[w] = wtot;
+  __syncthreads();
+  int pos = wpos;
+  for (int i = 0; i < w; ++i) pos += s_wsum[i];
+  int n_union = 0;
+#pragma unroll
+  for (int i = 0; i < LS_ATT_WAVES; ++i) n_union += s_wsum[i];
   const int32_t* vexp_seq = vexp + (int64_t)g * n_pages_ws + pg_off[b];
   const float inv_scale_log2 = 1.f / scale_log2;
-  __syncthreads();  // the union list and the ring counters are in place
+  // The pages are visited in a strided order (ascending page i goes to slot
+  // i * stride mod n_union, a bijection for stride coprime to n_union):
+  // neighbouring pages tend to be selected by the same rows, and spreading
+  // them out evens the work of the waves over any window of pages.
+  // (Empty or one-page lists keep stride 1; a coprime odd stride below 64 + 7
+  // exists for any list this kernel accepts, the loop bound only caps it.)
+  int stride = 1;
+  if (n_union > 1) {
+    for (int cand = 7; cand < 71; cand += 2) {
+      int a = cand, b = n_union;
+      while (b) {
+        const int t = a % b;
+        a = b;
+        b = t;
+      }
+      if (a == 1) {
+        stride = cand;
+        break;
+      }
+    }
+  }
+  while (word) {
+    const int bit = __ffs(word) - 1;
+    word &= word - 1;
+    const int page = tid * 32 + bit;
+    uint32_t rows = 0u;
+#pragma unroll
+    for (int i = 0; i < LS_ATT_TILE; ++i) rows |= ((row_word[i] >> bit) & 1u) << i;
+    const int dst = (int)(((uint32_t)pos * (uint32_t)stride) % (uint32_t)n_union);
+    int n_waves = 0;
+#pragma unroll
+    for (int i = 0; i < LS_ATT_WAVES; ++i) {
+      if (((rows >> (LS_ATT_TPW * i)) & ROWS_MASK) != 0u) {
+        ++n_waves;
+        atomicOr(&s_wneed[i][dst >> 5], 1u << (dst & 31));
+      }
+    }
+    s_umeta[dst] = ((uint32_t)page << 16) | rows;
+    s_uneed[dst] = (uint8_t)n_waves;
+    ++pos;
+  }
+
+  __syncthreads();  // the union list is complete and the bitmaps are dead, so
+                    // the ring may be written
   LS_WAIT_VMCNT(0);
+  // This wave's pages: bit b of lane l is set when one of its rows selected
+  // union page 32 l + b (the union holds at most 64 x 32 pages).
+  static_assert(LS_ATT_MAX_UNION <= 64 * 32, "one need word per lane");
+  const uint32_t wneed = lane < LS_ATT_MAX_UNION / 32 ? s_wneed[w][lane] : 0u;
 
   // ---- staging ----
   // One wave copies a whole union page into its stage: the page's staged
@@ -727,17 +664,15 @@ __global__ __launch_bounds__(64) void ls_bias_kernel(const typename LsElem<CT>::
 // ---------------------------------------------------------------------------
 namespace {
 struct AttnWs {
-  size_t kv, pg, tiles, vexp, cb, tok, plan, total;
-  int64_t lpad, n_pages, n_tiles;
+  size_t kv, pg, tiles, vexp, cb, tok, total;
+  int64_t lpad, n_pages;
 };
-AttnWs attn_ws(int64_t total_q, int64_t total_k, int batch, int G, int take, bool bias) {
+AttnWs attn_ws(int64_t total_k, int batch, int G, bool bias) {
   AttnWs L;
   L.n_pages = (total_k + 63) / 64 + batch;
   L.lpad = L.n_pages * 64;
-  L.n_tiles = (total_q + LS_ATT_TILE - 1) / LS_ATT_TILE + batch;
   size_t off = 0;
   L.kv = off; off += ls_align256((size_t)G * L.n_pages * LS_ATT_STAGE_BYTES);
-  L.plan = off; off += (size_t)G * L.n_tiles * ls_plan_layout(take).bytes;
   L.pg = off; off += ls_align256((size_t)(batch + 1) * 4);
   L.tiles = off; off += ls_align256((size_t)(batch + 1) * 4);
   L.vexp = off; off += ls_align256((size_t)G * L.n_pages * 4);
@@ -753,12 +688,12 @@ void launch_tile(dim3 grid, hipStream_t s, const void* q, int64_t q_rs, const ui
                  const int32_t* tok,
                  const int32_t* cu_q, const int32_t* cu_k, const int32_t* pg,
                  const int32_t* tiles, int batch, int64_t total_q, int G, int gs,
-                 const uint8_t* plan, int take, float scale_log2, int causal, void* out,
+                 const int32_t* topk_idx, int take, float scale_log2, int causal, void* out,
                  float* lse) {
   hipLaunchKernelGGL((ls_attn_tile_kernel<DT, BIAS>), grid, dim3(LS_ATT_THREADS), 0, s,
                      (const uint16_t*)q, q_rs, kv, L.lpad, vexp, cb, tok,
-                     L.n_pages, cu_q, cu_k, pg, tiles, batch, total_q, G, gs, plan, L.n_tiles,
-                     take, scale_log2, causal, (uint16_t*)out, lse, (int)(grid.x / 8));
+                     L.n_pages, cu_q, cu_k, pg, tiles, batch, total_q, G, gs, topk_idx, take,
+                     scale_log2, causal, (uint16_t*)out, lse, (int)(grid.x / 8));
 }
 
 // Shared body of the plain and the NOSA (cis != nullptr) entry points.
@@ -794,7 +729,7 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
                  q_row_stride % 8 == 0 && k_row_stride % 8 == 0 && v_row_stride % 8 == 0,
              LS_ERR_UNSUPPORTED,
              "%s: tensors must be 16-byte aligned with row strides %% 8 == 0", who);
-  const AttnWs L = attn_ws(total_q, total_k, batch, num_kv_heads, take, bias);
+  const AttnWs L = attn_ws(total_k, batch, num_kv_heads, bias);
   LS_REQUIRE(workspace && workspace_bytes >= L.total, LS_ERR_WORKSPACE,
              "%s: workspace needs %zu bytes", who, L.total);
   hipStream_t s = (hipStream_t)stream;
@@ -805,7 +740,6 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   int32_t* tiles = (int32_t*)(ws + L.tiles);
   float* cb = bias ? (float*)(ws + L.cb) : nullptr;
   int32_t* tok = (int32_t*)(ws + L.tok);
-  uint8_t* plan = (uint8_t*)(ws + L.plan);
   hipLaunchKernelGGL(ls_attn_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens_q, cu_seqlens_k,
                      batch, LS_ATT_TILE, pg, tiles, tok, LS_ATT_MAX_UNION + 1);
   int rc = ls_check_launch("ls_attn_plan_kernel");
@@ -837,15 +771,11 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   const int gs = num_heads / num_kv_heads;
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf((float)head_dim);
   const float scale_log2 = scale * 1.4426950408889634f;
-  const int64_t tile_bound = L.n_tiles;
-  hipLaunchKernelGGL(ls_attn_union_kernel, dim3((unsigned)tile_bound, num_kv_heads),
-                     dim3(LS_PLAN_THREADS), 0, s, cu_seqlens_q, cu_seqlens_k, tiles, batch,
-                     total_q, topk_idx, take, causal, plan, L.n_tiles);
-  if ((rc = ls_check_launch("ls_attn_union_kernel"))) return rc;
+  const int64_t tile_bound = (total_q + LS_ATT_TILE - 1) / LS_ATT_TILE + batch;
   const dim3 grid((unsigned)(8 * ((tile_bound + 7) / 8)), num_kv_heads, (gs + 15) / 16);
 #define LS_TILE_ARGS                                                                              \
   grid, s, q, q_row_stride, kv, L, vexp, cb, tok, cu_seqlens_q, cu_seqlens_k, pg,              \
-      tiles, batch, total_q, num_kv_heads, gs, plan, take, scale_log2, causal, out, lse
+      tiles, batch, total_q, num_kv_heads, gs, topk_idx, take, scale_log2, causal, out, lse
   if (dtype == LS_BF16) {
     if (bias) launch_tile<LS_BF16, true>(LS_TILE_ARGS);
     else launch_tile<LS_BF16, false>(LS_TILE_ARGS);
@@ -858,22 +788,22 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
 }
 }  // namespace
 
-extern "C" size_t ls_sparse_attn_workspace_size(int64_t total_q, int64_t total_k, int32_t batch,
+extern "C" size_t ls_sparse_attn_workspace_size(int64_t total_k, int32_t batch,
                                                 int32_t num_kv_heads, int32_t head_dim,
-                                                int32_t max_seqlen_k, int32_t take, int32_t dtype) {
+                                                int32_t max_seqlen_k, int32_t dtype) {
   (void)max_seqlen_k;
   (void)head_dim;
   (void)dtype;
-  return attn_ws(total_q, total_k, batch, num_kv_heads, take, false).total;
+  return attn_ws(total_k, batch, num_kv_heads, false).total;
 }
 
-extern "C" size_t ls_nosa_attn_workspace_size(int64_t total_q, int64_t total_k, int32_t batch,
+extern "C" size_t ls_nosa_attn_workspace_size(int64_t total_k, int32_t batch,
                                               int32_t num_kv_heads, int32_t head_dim,
-                                              int32_t max_seqlen_k, int32_t take, int32_t dtype) {
+                                              int32_t max_seqlen_k, int32_t dtype) {
   (void)max_seqlen_k;
   (void)head_dim;
   (void)dtype;
-  return attn_ws(total_q, total_k, batch, num_kv_heads, take, true).total;
+  return attn_ws(total_k, batch, num_kv_heads, true).total;
 }
 
 extern "C" int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const void* k,

@@ -216,8 +216,7 @@ def nosa_sparse_attention(
     lse = torch.empty((H, total_q), dtype=torch.float32, device=dev) if return_lse else None
     L = _hip.lib()
     dt = _hip.dtype_code(q.dtype)
-    ws = _hip.workspace(L.ls_nosa_attn_workspace_size(
-        total_q, total_k, batch, G, D, int(max_seqlen_k), topk_idx.shape[2], dt), dev)
+    ws = _hip.workspace(L.ls_nosa_attn_workspace_size(total_k, batch, G, D, int(max_seqlen_k), dt), dev)
     scale = -1.0 if softmax_scale is None else float(softmax_scale)
     rc = L.ls_nosa_attn_varlen(
         q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
