@@ -255,7 +255,7 @@ __device__ __forceinline__ void ls_nosa_topk_row(
     const void* __restrict__ P, int64_t prow, const float* __restrict__ cpg_seq, int n_scored,
     int out_len, int off_bq, int q_idx, int init_blocks, int local_blocks, int qk_select,
     int take, uint32_t pinf1, uint32_t ninf1, int lane, int32_t* __restrict__ orow,
-    uint32_t* __restrict__ scr) {
+    uint32_t* __restrict__ scr, const float* __restrict__ cpg_lds) {
   constexpr int NW = (NS + 31) / 32;
   // Every +inf (forced or shortlisted) and every -inf is one key, so ties among
   // them go to the lower page as in a stable sort.  Stage 1 keys come from the
@@ -290,10 +290,12 @@ __device__ __forceinline__ void ls_nosa_topk_row(
   for (int i = 0; i < NW; ++i) shortlist[i] = 0u;
   ls_mark_topk<NS>(key, ls_kth_key_row<NS, KEY32 ? 32 : 16>(key, qk_select, scr, lane), qk_select,
                    shortlist);
-  // Stage 2 keys.
+  // Stage 2 keys (the CIS page scores from the workgroup's LDS copy when its
+  // rows share a sequence and group).
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const int p = s * 64 + lane;
+    const float cis_lds = cpg_lds ? cpg_lds[p] : 0.f;
     uint32_t k;
     // The reference's order: pooled CIS scores with the forced overlay, then
     // pages after q_idx -inf, then the shortlist +inf.
@@ -302,7 +304,7 @@ __device__ __forceinline__ void ls_nosa_topk_row(
     else if (p > q_idx) k = ninf2;
     else if (p < init_blocks || (off_bq - local_blocks <= p && p <= off_bq)) k = pinf2;
     else if (p >= n_scored) k = ninf2;
-    else k = ls_order_key32(__builtin_bit_cast(uint32_t, cpg_seq[p])) >> SH2;
+    else k = ls_order_key32(__builtin_bit_cast(uint32_t, cpg_lds ? cis_lds : cpg_seq[p])) >> SH2;
     key[s] = k;
   }
   uint32_t chosen[NW];
@@ -331,11 +333,33 @@ __global__ __launch_bounds__(256) void ls_nosa_topk_kernel(
     int out_len, int init_blocks, int local_blocks, int qk_select, int take, int block_size,
     uint32_t pinf1, uint32_t ninf1, int32_t* __restrict__ topk_idx) {
   __shared__ uint32_t s_scr[4][256];  // per-wave gather space of the k-th key search
+  // The CIS page scores of the workgroup's sequence and group, when its four
+  // rows share them (all but the workgroups that straddle a boundary).
+  __shared__ __align__(16) float s_cpg[KPL * 64];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t row = (int64_t)blockIdx.x * 4 + wv;
-  if (row >= (int64_t)G * total_q) return;
+  const int64_t n_rows = (int64_t)G * total_q;
+  const int64_t row0 = (int64_t)blockIdx.x * 4;
+  const int64_t row_l = min(row0 + 3, n_rows - 1);
+  const int g0 = (int)(row0 / total_q), gl = (int)(row_l / total_q);
+  const int b0 = ls_find_segment(cu_q, batch, row0 - (int64_t)g0 * total_q);
+  const int bl = ls_find_segment(cu_q, batch, row_l - (int64_t)gl * total_q);
+  const bool shared_cis = g0 == gl && b0 == bl;
+  if (shared_cis) {
+    const int A0 = cu_a[b0 + 1] - cu_a[b0];
+    const int n_sc = min(A0 > 0 ? A0 / 4 + 1 : 0, out_len);
+    const int last = n_sc > 0 ? n_sc - 1 : 0;
+    const float* cs = cpg + (int64_t)g0 * cpg_g_stride + pg_off[b0];
+    const uint32_t base = (uint32_t)(uintptr_t)(ls_lds_void*)s_cpg;
+    for (int sl = wv; sl < (n_sc + 63) / 64; sl += 4)
+      ls_dma4(cs, 4u * (uint32_t)min(sl * 64 + lane, last), base + 256u * (uint32_t)sl);
+    LS_WAIT_VMCNT(0);
+  }
+  __syncthreads();
+  const int64_t row = row0 + wv;
+  if (row >= n_rows) return;
   uint32_t* const scr = s_scr[wv];
+  const float* const cpg_lds = shared_cis ? s_cpg : nullptr;
   const int g = (int)(row / total_q);
   const int64_t t = row - (int64_t)g * total_q;
   const int b = ls_find_segment(cu_q, batch, t);
@@ -350,14 +374,14 @@ __global__ __launch_bounds__(256) void ls_nosa_topk_kernel(
   int32_t* orow = topk_idx + row * take;
   const int64_t prow = row * p_stride;
   const int n_slots = (out_len + 63) >> 6;
-  if (n_slots <= 1) return ls_nosa_topk_row<1, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
-  if (n_slots <= 2) return ls_nosa_topk_row<2, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
-  if (n_slots <= 4 || KPL <= 4) return ls_nosa_topk_row<(KPL < 4 ? KPL : 4), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
-  if (n_slots <= 8 || KPL <= 8) return ls_nosa_topk_row<(KPL < 8 ? KPL : 8), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
-  if (n_slots <= 16 || KPL <= 16) return ls_nosa_topk_row<(KPL < 16 ? KPL : 16), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
-  if (n_slots <= 32 || KPL <= 32) return ls_nosa_topk_row<(KPL < 32 ? KPL : 32), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
-  if (n_slots <= 64 || KPL <= 64) return ls_nosa_topk_row<(KPL < 64 ? KPL : 64), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
-  return ls_nosa_topk_row<KPL, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr);
+  if (n_slots <= 1) return ls_nosa_topk_row<1, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
+  if (n_slots <= 2) return ls_nosa_topk_row<2, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
+  if (n_slots <= 4 || KPL <= 4) return ls_nosa_topk_row<(KPL < 4 ? KPL : 4), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
+  if (n_slots <= 8 || KPL <= 8) return ls_nosa_topk_row<(KPL < 8 ? KPL : 8), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
+  if (n_slots <= 16 || KPL <= 16) return ls_nosa_topk_row<(KPL < 16 ? KPL : 16), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
+  if (n_slots <= 32 || KPL <= 32) return ls_nosa_topk_row<(KPL < 32 ? KPL : 32), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
+  if (n_slots <= 64 || KPL <= 64) return ls_nosa_topk_row<(KPL < 64 ? KPL : 64), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
+  return ls_nosa_topk_row<KPL, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
 }
 
 template <bool KEY32, bool CIS32>
