@@ -10,6 +10,12 @@ object for the dominant kernel (block-sparse attention) measured with HIP
 events on the launch stream, per-stage timings, and the CPU oracle timed on a
 bounded row sample of the same workload on this host.
 
+``--workload minicpm41_8b_prefill_64k`` times a whole random-init
+MiniCPM4.1-8B-shaped prefill instead (32 layers, 65536 random token ids,
+LeanSelect at every layer, last-token logits): library GEMMs for the
+projections, HIP kernels for everything else.  Its line reports seconds per
+prefill and a per-stage breakdown of one layer.
+
 ``--variant nosa`` times the NOSA layer instead (budget 96 pages = 1 sink +
 16 local + 79 chosen, shortlist 41, CIS-biased attention) on the same shapes;
 its CPU baseline is not run (the oracle's broadcast CIS pooling alone would
@@ -37,6 +43,7 @@ WORKLOADS = {
     "minicpm41_8b_layer_128k": dict(seq_lens=(131072,)),
     "minicpm41_8b_layer_32k": dict(seq_lens=(32768,)),
     "minicpm41_8b_layer_ragged_8k_24k_48k_96k": dict(seq_lens=(8192, 24576, 49152, 98304)),
+    "minicpm41_8b_prefill_64k": dict(seq_lens=(65536,), model=True),
 }
 HBM_PEAK_GBS = 8000.0
 COPY_PROBE_BYTES = 1 << 30
@@ -144,6 +151,107 @@ def cpu_baseline(case, rows_per_seq: int, threads: int) -> dict:
     }
 
 
+def model_bench(args, dev) -> None:
+    """Whole-model prefill: seconds per prefill plus one layer's stage breakdown."""
+    import torch.nn.functional as F
+
+    from leanselect_amd import minicpm
+
+    wl = WORKLOADS[args.workload]
+    N = sum(wl["seq_lens"])
+    cfg = minicpm.MiniCPMConfig(topk=args.budget_pages or 64, local_blocks=args.local_blocks or 4)
+    print(f"[bench] building the random-init model ({cfg.num_hidden_layers} layers) ...",
+          file=sys.stderr, flush=True)
+    model = minicpm.MiniCPMLeanSelect(cfg, device=dev, seed=0)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    ids = torch.randint(0, cfg.vocab_size, (N,), generator=gen, device=dev, dtype=torch.int32)
+    cu_host = [0] + list(torch.tensor(wl["seq_lens"]).cumsum(0).tolist())
+    for _ in range(args.warmup):
+        model.prefill(ids, cu_host)
+    torch.cuda.synchronize()
+    print(f"[bench] warmup done, timing {args.steps} prefills", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        logits = model.prefill(ids, cu_host)
+    torch.cuda.synchronize()
+    s_step = (time.perf_counter() - t0) / args.steps
+    assert bool(torch.isfinite(logits).all()), "non-finite logits"
+
+    # Stage breakdown of layer 0 (HIP events on the launch stream).
+    from leanselect_amd.ops import compress_k, leanselect_prefill_topk_idx, sparse_attention
+
+    it = args.kernel_iters
+    H, G, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    L = model.layers[0]
+    cu = torch.tensor(cu_host, dtype=torch.int32, device=dev)
+    pos = model.positions(cu_host, dev)
+    x = minicpm.embed_scale(ids, model.embed, cfg.scale_emb)
+    h = minicpm.rms_layernorm(x, L.input_norm, cfg.rms_norm_eps)
+    qkv = F.linear(h, L.w_qkv)
+    cos, sin = model.rope_tables(max(wl["seq_lens"]))
+    minicpm.rope_inplace(qkv, pos, cos, sin, n_q_heads=H, n_k_heads=G, k_col_offset=H * D)
+    q = qkv[:, :H * D].view(N, H, D)
+    k = qkv[:, H * D:H * D + G * D].view(N, G, D)
+    v = qkv[:, H * D + G * D:].view(N, G, D)
+    kc, cu_c = compress_k(k, cu, cu_seqlens_host=cu_host)
+    kw = dict(topk=cfg.topk, init_blocks=cfg.init_blocks, local_blocks=cfg.local_blocks,
+              cu_seqlens_q_host=cu_host)
+    sel_ids = leanselect_prefill_topk_idx(q, kc, cu, cu_c, L.selector, **kw)
+    attn = sparse_attention(q, k, v, cu, cu, N, N, sel_ids)
+    o = F.linear(attn.view(N, H * D), L.w_o)
+    gu = F.linear(h, L.w_gate_up)
+    act = minicpm.silu_mul(gu, cfg.intermediate_size)
+    xs = x.clone()
+    stages = {
+        "rmsnorm": lambda: minicpm.rms_layernorm(x, L.input_norm, cfg.rms_norm_eps, out=h),
+        "qkv_gemm": lambda: F.linear(h, L.w_qkv),
+        "rope": lambda: minicpm.rope_inplace(qkv, pos, cos, sin, n_q_heads=H, n_k_heads=G,
+                                             k_col_offset=H * D, check_positions=False),
+        "compress_k": lambda: compress_k(k, cu, cu_seqlens_host=cu_host),
+        "select": lambda: leanselect_prefill_topk_idx(q, kc, cu, cu_c, L.selector, **kw),
+        "sparse_attention": lambda: sparse_attention(q, k, v, cu, cu, N, N, sel_ids),
+        "o_gemm": lambda: F.linear(attn.view(N, H * D), L.w_o),
+        "add_rmsnorm": lambda: minicpm.add_rms_layernorm(xs, o, 0.0, L.post_norm, cfg.rms_norm_eps, out=h),
+        "gate_up_gemm": lambda: F.linear(h, L.w_gate_up),
+        "silu_mul": lambda: minicpm.silu_mul(gu, cfg.intermediate_size, out=act),
+        "down_gemm": lambda: F.linear(act, L.w_down),
+    }
+    ms = {name: round(_event_ms(fn, it), 4) for name, fn in stages.items()}
+    n_keys = attention_keys(sel_ids, cu_host)
+    attn_flops = 4.0 * (H // G) * D * n_keys
+    hid, inter = cfg.hidden_size, cfg.intermediate_size
+    gemm_flops = 2.0 * N * hid * (H * D + 2 * G * D + H * D + 3 * inter)
+    gemm_ms = ms["qkv_gemm"] + ms["o_gemm"] + ms["gate_up_gemm"] + ms["down_gemm"]
+    result = {
+        "metric": "MiniCPM4.1-8B LeanSelect prefill seconds @64K (32 layers, B=1)",
+        "value": round(s_step, 4),
+        "unit": "s/prefill",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * s_step, 2),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (uniform random token ids, random-init weights)",
+        "config": {
+            "workload": args.workload, "seq_lens": list(wl["seq_lens"]),
+            "layers": cfg.num_hidden_layers, "hidden": hid, "ffn": inter,
+            "vocab": cfg.vocab_size, "heads_q": H, "heads_kv": G, "head_dim": D,
+            "budget_pages": cfg.topk, "sink_pages": cfg.init_blocks,
+            "local_blocks": cfg.local_blocks, "router": f"{cfg.router_heads}x{cfg.router_dim}",
+            "rope": "plain, base 10000", "parallelism": "single-gpu",
+        },
+        "layer0_stages_ms": ms,
+        "layer0_gemm_tflops": round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 1),
+        "layer0_attention_tflops": round(attn_flops / (ms["sparse_attention"] * 1e-3) / 1e12, 1),
+        "reference_published": ("H200, real weights, budget 96 pages (32 local blocks), LongRoPE: "
+                                "3.603 s at 64K (results/minicpm_efficiency.json)"),
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -154,6 +262,10 @@ def main() -> None:
     ap.add_argument("--kernel-iters", type=int, default=5)
     ap.add_argument("--cpu-rows-per-seq", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--budget-pages", type=int, default=None,
+                    help="model prefill only: total page budget (default 64)")
+    ap.add_argument("--local-blocks", type=int, default=None,
+                    help="model prefill only: local blocks (default 4)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run one plain copy of COPY_PROBE_BYTES and one step, untimed (for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -167,6 +279,9 @@ def main() -> None:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     wl = WORKLOADS[args.workload]
+    if wl.get("model"):
+        model_bench(args, dev)
+        return
     print(f"[bench] generating {args.workload} ...", file=sys.stderr, flush=True)
     nosa = args.variant == "nosa"
     if nosa:  # NOSA budget: topk 80 + 16 local, select_blocks 24 (nosa.py:643-676)

@@ -292,6 +292,69 @@ int ls_nosa_attn_varlen(const void* q, int64_t q_row_stride, const void* k, int6
                         float softmax_scale, void* out, float* lse, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Decoder-layer producers and consumers of the LeanSelect attention layer
+ * (MiniCPM4.1 prefill, leanselect/models/minicpm.py:3562-3630).  16-bit
+ * dtypes only; rows are `*_row_stride` elements apart; every tensor is
+ * 16-byte aligned.  Each output element is rounded where the reference's
+ * torch expression rounds.
+ * ------------------------------------------------------------------------ */
+
+/*
+ * RMSNorm: out = round(round(x * (1 / sqrt(mean(x^2) + eps))) * weight), the
+ * statistics in float32.  x, out [n_rows, hidden]; weight [hidden].
+ * hidden is a multiple of 8 up to 8192.
+ * Replaces rms_layernorm (leanselect/models/minicpm.py:772-788).
+ */
+int ls_rmsnorm(const void* x, int64_t x_row_stride, const void* weight, int64_t n_rows,
+               int32_t hidden, float eps, int32_t dtype, void* out, int64_t out_row_stride,
+               void* stream);
+
+/*
+ * Scaled residual add fused with the next RMSNorm:
+ *   residual = round(residual + round(h * h_scale))   (in place)
+ *   out      = RMSNorm(residual) as ls_rmsnorm.
+ * Replaces `residual + hidden_states * (scale_depth / sqrt(num_layers))`
+ * followed by the next MiniCPMRMSNorm (leanselect/models/minicpm.py:3616-3625,
+ * 3578; the last layer's add feeds the model's final norm, 3698).
+ */
+int ls_add_rmsnorm(void* residual, int64_t res_row_stride, const void* h, int64_t h_row_stride,
+                   float h_scale, const void* weight, int64_t n_rows, int32_t hidden, float eps,
+                   int32_t dtype, void* out, int64_t out_row_stride, void* stream);
+
+/*
+ * Rotary embedding in place on the query heads (columns [0, n_q_heads *
+ * head_dim)) and key heads (columns k_col_offset + [0, n_k_heads * head_dim))
+ * of each row: x = round(x * cos[p] + rotate_half(x) * sin[p]) in float32
+ * (no fused multiply-add), p = positions[row] (int32, 0 <= p < table_rows;
+ * the kernel clamps out-of-range values).  cos_table / sin_table are float32
+ * [table_rows, head_dim].  head_dim must be 128.
+ * Replaces apply_rotary_pos_emb on the q/k projections
+ * (leanselect/models/minicpm.py:1027-1070, called at 2218-2222).
+ */
+int ls_rope_inplace(void* x, int64_t row_stride, const int32_t* positions, int64_t n_rows,
+                    int32_t n_q_heads, int32_t n_k_heads, int64_t k_col_offset, int32_t head_dim,
+                    const float* cos_table, const float* sin_table, int64_t table_rows,
+                    int32_t dtype, void* stream);
+
+/*
+ * SiLU-gated activation: out = round(round(silu(g)) * u), g = columns
+ * [0, inter) and u = columns [inter, 2 inter) of gate_up.
+ * Replaces act_fn(gate_proj(x)) * up_proj(x) in MiniCPMMLP.forward
+ * (leanselect/models/minicpm.py:1098-1135).
+ */
+int ls_silu_mul(const void* gate_up, int64_t gu_row_stride, int64_t n_rows, int32_t inter,
+                int32_t dtype, void* out, int64_t out_row_stride, void* stream);
+
+/*
+ * Scaled token embedding: out[n] = round(table[ids[n]] * scale), out
+ * [n, hidden] contiguous; ids int32 in [0, vocab) (clamped otherwise).
+ * Replaces `embed_tokens(input_ids) * scale_emb`
+ * (leanselect/models/minicpm.py:3773-3774).
+ */
+int ls_embed_scale(const int32_t* ids, int64_t n, const void* table, int64_t vocab,
+                   int32_t hidden, float scale, int32_t dtype, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

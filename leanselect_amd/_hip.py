@@ -59,6 +59,13 @@ SIGNATURES = {
     "ls_nosa_attn_varlen": (
         _i32, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32, _p, _p, _i32, _i64, _i64, _i32,
                _i32, _i32, _i32, _i32, _i32, _p, _i32, _i32, _f32, _p, _p, _p, _sz, _p]),
+    "ls_rmsnorm": (_i32, [_p, _i64, _p, _i64, _i32, _f32, _i32, _p, _i64, _p]),
+    "ls_add_rmsnorm": (
+        _i32, [_p, _i64, _p, _i64, _f32, _p, _i64, _i32, _f32, _i32, _p, _i64, _p]),
+    "ls_rope_inplace": (
+        _i32, [_p, _i64, _p, _i64, _i32, _i32, _i64, _i32, _p, _p, _i64, _i32, _p]),
+    "ls_silu_mul": (_i32, [_p, _i64, _i64, _i32, _i32, _p, _i64, _p]),
+    "ls_embed_scale": (_i32, [_p, _i64, _p, _i64, _i32, _f32, _i32, _p, _p]),
 }
 
 _lib = None

@@ -38,6 +38,9 @@ FILE_FLAGS = {
     # MFMAs accumulate in ordinary VGPRs, so their results need no copies out
     # of the accumulation registers before the pooling reads them.
     "ls_select": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mno-amdgpu-ieee", "-fno-honor-nans"],
+    # The decoder kernels round every float32 product and sum separately, as
+    # the reference's torch expressions do.
+    "ls_model": ["-ffp-contract=off"],
 }
 
 

@@ -1,0 +1,333 @@
+"""MiniCPM4.1-shaped prefill with LeanSelect attention at every layer (GPU only).
+
+Follows ``MiniCPMForCausalLM``'s prefill with ``--method leanselect`` and
+``dense_len = -1`` (every layer sparse): the decoder layer
+(leanselect/models/minicpm.py:3562-3630), its attention
+(``MiniCPMInfLLMv2Attention.forward``, 2146-2377, LeanSelect branch of
+``_sparse_attention_forward``, 2389-2772), the model loop (3708-3837) and the
+last-token LM head (3987-4090).  Projections are plain library GEMMs
+(``torch.nn.functional.linear`` on hipBLASLt); RMSNorm, the scaled residual add,
+rotary embedding, the SiLU-gated activation and the scaled embedding are HIP
+kernels of ``libleanselect_hip.so``; attention is
+:func:`leanselect_amd.prefill.leanselect_sparse_prefill`.
+
+Layout choices: the q/k/v projections are one GEMM into a packed ``[N, H*D +
+2*G*D]`` buffer; the rotary embedding runs in place on it, and the attention
+layer reads q, k and v as strided views of that buffer (no copies).  The
+residual stream is updated in place by the fused add + RMSNorm kernel, whose
+normalised output feeds the next GEMM.
+
+Weights are random-initialised (no checkpoint is loaded here).  Nothing in this
+module falls back to a non-HIP path: it raises when the library is missing or
+the tensors are not on a GPU.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import _hip
+from .prefill import leanselect_sparse_prefill
+from .selector import LeanSelectSelector
+
+__all__ = [
+    "MiniCPMConfig",
+    "MiniCPMLeanSelect",
+    "rotary_tables",
+    "rms_layernorm",
+    "add_rms_layernorm",
+    "rope_inplace",
+    "silu_mul",
+    "embed_scale",
+]
+
+
+@dataclass
+class MiniCPMConfig:
+    """Architecture and LeanSelect geometry.
+
+    Defaults are the MiniCPM4.1-8B shape (hidden 4096, 32 layers, 32 query / 2
+    KV heads of 128, FFN 16384, vocabulary 73448) with its published
+    ``scale_emb`` 12, ``scale_depth`` 1.4 and ``dim_model_base`` 256 (the
+    reference's ``MiniCPMConfig`` defaults are 1, 1, 1:
+    leanselect/models/configuration_minicpm.py:130-132), plain RoPE base 10000,
+    and the LeanSelect geometry of configs/minicpm.json with a 64-page budget
+    (1 sink page, 4 local blocks).
+    """
+
+    hidden_size: int = 4096
+    num_hidden_layers: int = 32
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 2
+    intermediate_size: int = 16384
+    vocab_size: int = 73448
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 10000.0
+    scale_emb: float = 12.0
+    scale_depth: float = 1.4
+    dim_model_base: int = 256
+    topk: int = 64             # total page budget, forced pages included
+    init_blocks: int = 1
+    local_blocks: int = 4
+    block_size: int = 64
+    kernel_size: int = 32
+    kernel_stride: int = 16
+    router_heads: int = 4
+    router_dim: int = 32
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+
+# ---------------------------------------------------------------------------
+# Kernel wrappers (HIP; 16-bit tensors on one GPU)
+# ---------------------------------------------------------------------------
+def _rows(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.ndim != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D tensor with unit column stride")
+    return t
+
+
+def rotary_tables(head_dim: int, max_pos: int, base: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """float32 ``(cos, sin)`` ``[max_pos, head_dim]`` built like
+    ``MiniCPMRotaryEmbedding._set_cos_sin_cache`` (minicpm.py:804-838)."""
+    inv_freq = 1.0 / base ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim)
+    t = torch.arange(max_pos, device=device, dtype=inv_freq.dtype)
+    emb = torch.cat((torch.outer(t, inv_freq),) * 2, dim=-1)
+    return emb.cos().contiguous(), emb.sin().contiguous()
+
+
+def rms_layernorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """``rms_layernorm`` (minicpm.py:772-788) of the rows of ``x [n, hidden]``."""
+    _rows(x, "x")
+    dev = _hip.require_gpu(x, weight)
+    n, hidden = x.shape
+    if weight.shape != (hidden,) or weight.dtype != x.dtype:
+        raise ValueError("weight must be [hidden] in x's dtype")
+    out = torch.empty_like(x, memory_format=torch.contiguous_format) if out is None else _rows(out, "out")
+    _hip.check(_hip.lib().ls_rmsnorm(
+        x.data_ptr(), x.stride(0), weight.contiguous().data_ptr(), n, hidden, float(eps),
+        _hip.dtype_code(x.dtype), out.data_ptr(), out.stride(0), _hip.stream_of(dev)), "ls_rmsnorm")
+    return out
+
+
+def add_rms_layernorm(residual: torch.Tensor, h: torch.Tensor, h_scale: float,
+                      weight: torch.Tensor, eps: float,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """``residual += h * h_scale`` (in place, rounded like minicpm.py:3616-3625),
+    then the RMSNorm of the new residual (returned)."""
+    _rows(residual, "residual")
+    _rows(h, "h")
+    dev = _hip.require_gpu(residual, h, weight)
+    n, hidden = residual.shape
+    if h.shape != residual.shape or h.dtype != residual.dtype:
+        raise ValueError("h must match residual's shape and dtype")
+    if weight.shape != (hidden,) or weight.dtype != residual.dtype:
+        raise ValueError("weight must be [hidden] in residual's dtype")
+    out = torch.empty((n, hidden), dtype=residual.dtype, device=dev) if out is None else _rows(out, "out")
+    _hip.check(_hip.lib().ls_add_rmsnorm(
+        residual.data_ptr(), residual.stride(0), h.data_ptr(), h.stride(0), float(h_scale),
+        weight.contiguous().data_ptr(), n, hidden, float(eps), _hip.dtype_code(residual.dtype),
+        out.data_ptr(), out.stride(0), _hip.stream_of(dev)), "ls_add_rmsnorm")
+    return out
+
+
+def rope_inplace(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                 *, n_q_heads: int, n_k_heads: int, k_col_offset: int, head_dim: int = 128,
+                 check_positions: bool = True) -> torch.Tensor:
+    """``apply_rotary_pos_emb`` (minicpm.py:1034-1070) in place on the query heads
+    (columns ``[0, n_q_heads*head_dim)``) and key heads (from ``k_col_offset``) of
+    each row of ``x [n, width]``; ``positions`` int32 ``[n]``."""
+    _rows(x, "x")
+    dev = _hip.require_gpu(x, positions, cos, sin)
+    if positions.dtype != torch.int32 or positions.shape != (x.shape[0],):
+        raise ValueError("positions must be int32 [n]")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape \
+            or cos.ndim != 2 or cos.shape[1] != head_dim:
+        raise ValueError("cos/sin must be float32 [table_rows, head_dim]")
+    if check_positions and positions.numel():
+        lo, hi = int(positions.min()), int(positions.max())
+        if lo < 0 or hi >= cos.shape[0]:
+            raise ValueError(f"positions must lie in [0, {cos.shape[0]}) (got {lo}..{hi})")
+    _hip.check(_hip.lib().ls_rope_inplace(
+        x.data_ptr(), x.stride(0), positions.contiguous().data_ptr(), x.shape[0], n_q_heads,
+        n_k_heads, k_col_offset, head_dim, cos.contiguous().data_ptr(), sin.contiguous().data_ptr(),
+        cos.shape[0], _hip.dtype_code(x.dtype), _hip.stream_of(dev)), "ls_rope_inplace")
+    return x
+
+
+def silu_mul(gate_up: torch.Tensor, inter: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(gate) * up`` for ``gate_up [n, 2*inter]`` = [gate | up] (minicpm.py:1098-1135)."""
+    _rows(gate_up, "gate_up")
+    dev = _hip.require_gpu(gate_up)
+    n = gate_up.shape[0]
+    if gate_up.shape[1] < 2 * inter:
+        raise ValueError("gate_up must hold 2*inter columns")
+    out = torch.empty((n, inter), dtype=gate_up.dtype, device=dev) if out is None else _rows(out, "out")
+    _hip.check(_hip.lib().ls_silu_mul(
+        gate_up.data_ptr(), gate_up.stride(0), n, inter, _hip.dtype_code(gate_up.dtype),
+        out.data_ptr(), out.stride(0), _hip.stream_of(dev)), "ls_silu_mul")
+    return out
+
+
+def embed_scale(ids: torch.Tensor, table: torch.Tensor, scale: float,
+                check_ids: bool = True) -> torch.Tensor:
+    """``embed_tokens(ids) * scale_emb`` (minicpm.py:3773-3774); ``ids`` int32 [n]."""
+    dev = _hip.require_gpu(ids, table)
+    if ids.dtype != torch.int32 or ids.ndim != 1:
+        raise ValueError("ids must be int32 [n]")
+    if table.ndim != 2 or not table.is_contiguous():
+        raise ValueError("table must be a contiguous [vocab, hidden] tensor")
+    if check_ids and ids.numel():
+        lo, hi = int(ids.min()), int(ids.max())
+        if lo < 0 or hi >= table.shape[0]:
+            raise IndexError(f"token ids must lie in [0, {table.shape[0]}) (got {lo}..{hi})")
+    out = torch.empty((ids.numel(), table.shape[1]), dtype=table.dtype, device=dev)
+    _hip.check(_hip.lib().ls_embed_scale(
+        ids.contiguous().data_ptr(), ids.numel(), table.data_ptr(), table.shape[0], table.shape[1],
+        float(scale), _hip.dtype_code(table.dtype), out.data_ptr(), _hip.stream_of(dev)),
+        "ls_embed_scale")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# The model
+# ---------------------------------------------------------------------------
+class _Layer:
+    __slots__ = ("input_norm", "w_qkv", "w_o", "post_norm", "w_gate_up", "w_down", "selector")
+
+
+class MiniCPMLeanSelect:
+    """Random-initialised MiniCPM4.1-shaped decoder with LeanSelect prefill attention.
+
+    Linear weights ~ N(0, weight_std^2) in ``dtype``; norm weights 1 + N(0, 0.1^2);
+    selectors use ``LeanSelectSelector.reset_parameters`` (torch's RNG seeded per
+    layer).  ``prefill`` returns float32 last-token logits per sequence.
+    """
+
+    def __init__(self, cfg: MiniCPMConfig, *, device="cuda", dtype=torch.bfloat16,
+                 seed: int = 0, weight_std: float = 0.02):
+        if dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("the model runs in bf16 or fp16")
+        if cfg.head_dim != 128:
+            raise ValueError("the attention kernels need head_dim 128")
+        self.cfg, self.dtype = cfg, dtype
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError("MiniCPMLeanSelect runs on the GPU")
+        g = torch.Generator(device=self.device).manual_seed(seed)
+        H, G, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        hid, inter = cfg.hidden_size, cfg.intermediate_size
+
+        def lin(out_f, in_f):
+            return torch.empty(out_f, in_f, dtype=dtype, device=self.device).normal_(
+                0.0, weight_std, generator=g)
+
+        def norm_w():
+            w = torch.empty(hid, dtype=torch.float32, device=self.device).normal_(0.0, 0.1, generator=g)
+            return (1.0 + w).to(dtype)
+
+        self.embed = lin(cfg.vocab_size, hid)
+        self.layers = []
+        for li in range(cfg.num_hidden_layers):
+            L = _Layer()
+            L.input_norm = norm_w()
+            L.w_qkv = lin(H * D + 2 * G * D, hid)
+            L.w_o = lin(hid, H * D)
+            L.post_norm = norm_w()
+            L.w_gate_up = lin(2 * inter, hid)
+            L.w_down = lin(hid, inter)
+            torch.manual_seed(seed * 1000 + li)
+            sel = LeanSelectSelector(num_heads=H, num_kv_heads=G, head_dim=D,
+                                     router_heads=cfg.router_heads, router_dim=cfg.router_dim)
+            L.selector = sel.requires_grad_(False).to(self.device)
+            self.layers.append(L)
+        self.final_norm = norm_w()
+        self.lm_head = lin(cfg.vocab_size, hid)
+        self._rope = None
+
+    # -- pieces ----------------------------------------------------------------
+    def rope_tables(self, max_pos: int):
+        if self._rope is None or self._rope[0].shape[0] < max_pos:
+            self._rope = rotary_tables(self.cfg.head_dim, max_pos, self.cfg.rope_theta, self.device)
+        return self._rope
+
+    @property
+    def residual_scale(self) -> float:
+        return self.cfg.scale_depth / math.sqrt(self.cfg.num_hidden_layers)
+
+    def attention(self, li: int, h: torch.Tensor, positions: torch.Tensor, cu_seqlens: torch.Tensor,
+                  cu_host: list[int], return_parts: bool = False):
+        """Attention block of layer ``li`` on the normalised input ``h [N, hidden]``.
+
+        q/k/v projection (one GEMM), rotary embedding in place, LeanSelect sparse
+        prefill on strided views of the projection output, output projection.
+        """
+        cfg, L = self.cfg, self.layers[li]
+        H, G, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        N = h.shape[0]
+        qkv = F.linear(h, L.w_qkv)
+        cos, sin = self.rope_tables(max(cu_host[i + 1] - cu_host[i] for i in range(len(cu_host) - 1)))
+        rope_inplace(qkv, positions, cos, sin, n_q_heads=H, n_k_heads=G, k_col_offset=H * D,
+                     head_dim=D, check_positions=False)
+        q = qkv[:, : H * D].view(N, H, D)
+        k = qkv[:, H * D: H * D + G * D].view(N, G, D)
+        v = qkv[:, H * D + G * D:].view(N, G, D)
+        attn, ids = leanselect_sparse_prefill(
+            q, k, v, cu_seqlens, L.selector, topk=cfg.topk, local_blocks=cfg.local_blocks,
+            init_blocks=cfg.init_blocks, block_size=cfg.block_size, kernel_size=cfg.kernel_size,
+            kernel_stride=cfg.kernel_stride, cu_seqlens_host=cu_host, return_topk_idx=True)
+        o = F.linear(attn.view(N, H * D), L.w_o)
+        if return_parts:
+            return o, dict(qkv=qkv, attn=attn, topk_idx=ids)
+        return o
+
+    def mlp(self, li: int, h: torch.Tensor) -> torch.Tensor:
+        """``down(silu(gate(h)) * up(h))`` with gate and up as one GEMM."""
+        L = self.layers[li]
+        return F.linear(silu_mul(F.linear(h, L.w_gate_up), self.cfg.intermediate_size), L.w_down)
+
+    @staticmethod
+    def positions(cu_host: list[int], device) -> torch.Tensor:
+        """int32 position of each packed token inside its sequence."""
+        parts = [torch.arange(cu_host[i + 1] - cu_host[i], dtype=torch.int32)
+                 for i in range(len(cu_host) - 1)]
+        return torch.cat(parts).to(device)
+
+    # -- prefill -----------------------------------------------------------------
+    @torch.no_grad()
+    def prefill(self, input_ids: torch.Tensor, cu_seqlens_host: list[int] | None = None,
+                *, layer_hook=None) -> torch.Tensor:
+        """Last-token logits ``[B, vocab]`` (float32) of packed sequences.
+
+        ``input_ids`` int32 ``[N]`` on the GPU; ``cu_seqlens_host`` the packed
+        offsets (one sequence of N tokens when omitted).  ``layer_hook(li, x)``,
+        if given, sees the residual stream after each layer.
+        """
+        cfg = self.cfg
+        N = input_ids.numel()
+        cu_host = list(cu_seqlens_host) if cu_seqlens_host is not None else [0, N]
+        if cu_host[0] != 0 or cu_host[-1] != N or any(b < a for a, b in zip(cu_host, cu_host[1:])):
+            raise ValueError("cu_seqlens_host must be non-decreasing from 0 to the token count")
+        dev = _hip.require_gpu(input_ids)
+        cu = torch.tensor(cu_host, dtype=torch.int32, device=dev)
+        pos = self.positions(cu_host, dev)
+        x = embed_scale(input_ids, self.embed, cfg.scale_emb)
+        h = rms_layernorm(x, self.layers[0].input_norm, cfg.rms_norm_eps)
+        c = self.residual_scale
+        for li in range(cfg.num_hidden_layers):
+            o = self.attention(li, h, pos, cu, cu_host)
+            add_rms_layernorm(x, o, c, self.layers[li].post_norm, cfg.rms_norm_eps, out=h)
+            d = self.mlp(li, h)
+            nxt = self.layers[li + 1].input_norm if li + 1 < cfg.num_hidden_layers else self.final_norm
+            add_rms_layernorm(x, d, c, nxt, cfg.rms_norm_eps, out=h)
+            if layer_hook is not None:
+                layer_hook(li, x)
+        last = torch.tensor([b - 1 for b in cu_host[1:]], device=dev, dtype=torch.long)
+        h_last = h.index_select(0, last) / (cfg.hidden_size / cfg.dim_model_base)
+        return F.linear(h_last, self.lm_head).float()

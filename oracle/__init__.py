@@ -11,3 +11,4 @@ here.
 from .leanselect_oracle import *  # noqa: F401,F403
 from .check import *  # noqa: F401,F403
 from .nosa_oracle import *  # noqa: F401,F403
+from .minicpm_oracle import *  # noqa: F401,F403
