@@ -43,8 +43,14 @@ WORKLOADS = {
     "minicpm41_8b_layer_128k": dict(seq_lens=(131072,)),
     "minicpm41_8b_layer_32k": dict(seq_lens=(32768,)),
     "minicpm41_8b_layer_ragged_8k_24k_48k_96k": dict(seq_lens=(8192, 24576, 49152, 98304)),
+    "minicpm41_8b_prefill_32k": dict(seq_lens=(32768,), model=True),
     "minicpm41_8b_prefill_64k": dict(seq_lens=(65536,), model=True),
+    "minicpm41_8b_prefill_128k": dict(seq_lens=(131072,), model=True),
 }
+# Published whole-model LeanSelect prefill times of the reference (H200, real
+# weights, budget 96 pages with 32 local blocks, LongRoPE, median of 10 runs;
+# results/minicpm_efficiency.json), for context beside the model workloads.
+REFERENCE_PREFILL_S = {32768: 1.745, 65536: 3.603, 131072: 7.954}
 HBM_PEAK_GBS = 8000.0
 COPY_PROBE_BYTES = 1 << 30
 # HBM bytes per launch of the attention kernel, from rocprofv3 FETCH_SIZE and
@@ -223,7 +229,7 @@ def model_bench(args, dev) -> None:
     gemm_flops = 2.0 * N * hid * (H * D + 2 * G * D + H * D + 3 * inter)
     gemm_ms = ms["qkv_gemm"] + ms["o_gemm"] + ms["gate_up_gemm"] + ms["down_gemm"]
     result = {
-        "metric": "MiniCPM4.1-8B LeanSelect prefill seconds @64K (32 layers, B=1)",
+        "metric": f"MiniCPM4.1-8B LeanSelect prefill seconds @{N // 1024}K (32 layers, B=1)",
         "value": round(s_step, 4),
         "unit": "s/prefill",
         "n_gpus": 1,
@@ -246,8 +252,9 @@ def model_bench(args, dev) -> None:
         "layer0_stages_ms": ms,
         "layer0_gemm_tflops": round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 1),
         "layer0_attention_tflops": round(attn_flops / (ms["sparse_attention"] * 1e-3) / 1e12, 1),
-        "reference_published": ("H200, real weights, budget 96 pages (32 local blocks), LongRoPE: "
-                                "3.603 s at 64K (results/minicpm_efficiency.json)"),
+        "reference_published": (f"H200, real weights, budget 96 pages (32 local blocks), LongRoPE: "
+                                f"{REFERENCE_PREFILL_S[N]} s (results/minicpm_efficiency.json)"
+                                if N in REFERENCE_PREFILL_S and len(wl['seq_lens']) == 1 else None),
     }
     print(json.dumps(result), flush=True)
 
