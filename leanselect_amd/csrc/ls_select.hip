@@ -109,9 +109,9 @@ __global__ __launch_bounds__(256) void ls_proj_mfma_kernel(
 // a workgroup owns 128 rows x F columns, the weight tile of each 128-wide K
 // step is staged once in LDS (double buffered, 16-byte chunks XOR-swizzled by
 // column) and shared by the four waves, and each wave prefetches its next A
-// step while the MFMAs of the current one run.  The reduction index is
-// permuted inside a K step: lane group q takes k = 32q + 8ks .. +7 in slice
-// ks, for both operands, so every lane reads 64 contiguous bytes of its A row.
+// step while the MFMAs of the current one run.  In slice ks of a K step, lane
+// group q takes k = 32ks + 8q .. +7 (both operands), so the four lanes of a
+// row read 64 contiguous bytes per load instruction.
 // Requires K % 128 == 0.
 template <int DT, int FB>
 __global__ __launch_bounds__(256, 2) void ls_proj_tile_kernel(
@@ -126,8 +126,8 @@ __global__ __launch_bounds__(256, 2) void ls_proj_tile_kernel(
   const int64_t m0 = (int64_t)blockIdx.x * 128 + w * 32;
   const uint16_t* Ag = A + g * gk;
   const uint16_t* Wg = wt + (int64_t)g * F * K;
-  const uint16_t* a0p = Ag + min(m0 + r, M - 1) * lda + 32 * q;
-  const uint16_t* a1p = Ag + min(m0 + 16 + r, M - 1) * lda + 32 * q;
+  const uint16_t* a0p = Ag + min(m0 + r, M - 1) * lda + 8 * q;
+  const uint16_t* a1p = Ag + min(m0 + 16 + r, M - 1) * lda + 8 * q;
   const int nk = K / 128;
 
   ls_u32x4 breg[NB];
@@ -149,8 +149,8 @@ __global__ __launch_bounds__(256, 2) void ls_proj_tile_kernel(
   auto load_a = [&](int kt) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      a0[ks] = ls_load16(a0p + 128 * kt + 8 * ks);
-      a1[ks] = ls_load16(a1p + 128 * kt + 8 * ks);
+      a0[ks] = ls_load16(a0p + 128 * kt + 32 * ks);
+      a1[ks] = ls_load16(a1p + 128 * kt + 32 * ks);
     }
   };
 
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256, 2) void ls_proj_tile_kernel(
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int c = 0; c < FB; ++c) {
-        const ls_u32x4 b = sB[buf][(16 * c + r) * 16 + ((4 * q + ks) ^ r)];
+        const ls_u32x4 b = sB[buf][(16 * c + r) * 16 + ((4 * ks + q) ^ r)];
         acc0[c] = LsElem<DT>::mfma(c0[ks], b, acc0[c]);
         acc1[c] = LsElem<DT>::mfma(c1[ks], b, acc1[c]);
       }
@@ -1128,8 +1128,10 @@ extern "C" int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t to
              "ls_select_prefill: take must be min(topk, ceil(max_seqlen_q / block_size)) = %d",
              topk < max_pages ? topk : max_pages);
   if (total_q == 0 || batch == 0 || take == 0) return LS_OK;
-  LS_REQUIRE(q && kc && cu_seqlens_q && cu_seqlens_kc && topk_idx, LS_ERR_INVALID,
-             "ls_select_prefill: null pointer");
+  // kc may be null only when there is no compressed key at all (every sequence
+  // shorter than one window: its rows get no pages, as the reference skips it).
+  LS_REQUIRE(q && (kc || total_atoms == 0) && cu_seqlens_q && cu_seqlens_kc && topk_idx,
+             LS_ERR_INVALID, "ls_select_prefill: null pointer");
   const int eb = (int)ls_dtype_bytes(dtype);
   const int F = router_heads * router_dim, G = num_kv_heads, gs = num_heads / num_kv_heads;
   const WsLayout L = ws_layout(total_q, total_atoms, batch, num_heads, G, head_dim, F,
@@ -1212,7 +1214,8 @@ extern "C" int ls_nosa_select_prefill(
   LS_REQUIRE(take == want, LS_ERR_INVALID,
              "ls_nosa_select_prefill: take must be min(topk, ceil(max_seqlen_q / 64)) = %d", want);
   if (total_q == 0 || batch == 0 || take == 0) return LS_OK;
-  LS_REQUIRE(q && kc && cis && cu_seqlens_q && cu_seqlens_kc && cu_seqlens_k && topk_idx,
+  LS_REQUIRE(q && (kc || total_atoms == 0) && cis && cu_seqlens_q && cu_seqlens_kc &&
+                 cu_seqlens_k && topk_idx,
              LS_ERR_INVALID, "ls_nosa_select_prefill: null pointer");
   const int qk_sel_raw = init_blocks + local_blocks + select_blocks;
   const int qk_select = qk_sel_raw < out_len ? qk_sel_raw : out_len;

@@ -79,6 +79,8 @@ def nosa_mean_pooling(cis_score: torch.Tensor, cu_seqlens, max_seqlen: int,
 
 def _pool_pages(x: torch.Tensor, lk: int, out_len: int, s: int) -> torch.Tensor:
     """Max of ``x[..., j]`` over ``j in [p*s - 1, p*s + s) ∩ [0, lk)`` for ``p < out_len``."""
+    if x.shape[-1] == 0:  # no window at all: every page pools an empty range
+        return torch.full((*x.shape[:-1], out_len), float("-inf"), dtype=x.dtype)
     idx = torch.arange(out_len)[:, None] * s - 1 + torch.arange(s + 1)[None, :]
     valid = (idx >= 0) & (idx < lk)
     g = x[..., idx.clamp(0, max(x.shape[-1] - 1, 0))]

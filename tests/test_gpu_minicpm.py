@@ -194,3 +194,27 @@ def test_prefill_rejects_bad_offsets():
     ids = torch.zeros(100, dtype=torch.int32, device=DEV)
     with pytest.raises(ValueError):
         model.prefill(ids, [0, 50])
+
+
+def test_prefill_ragged_with_short_sequences_and_wide_local_window():
+    """Sequences shorter than one compression window (no compressed key: plans of
+    only the forced pages) beside longer ones, under a budget with a wide local
+    window as in the reference's published setting (a third of the budget local)."""
+    cfg = minicpm.MiniCPMConfig(hidden_size=1024, num_hidden_layers=2, num_attention_heads=8,
+                                num_key_value_heads=2, intermediate_size=2048, vocab_size=1000,
+                                topk=24, local_blocks=8)
+    model = minicpm.MiniCPMLeanSelect(cfg, device=DEV, seed=7)
+    gen = torch.Generator(device=DEV).manual_seed(8)
+    lens = [20, 1300, 64, 1]
+    seqs = [torch.randint(0, cfg.vocab_size, (n,), generator=gen, device=DEV, dtype=torch.int32)
+            for n in lens]
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    packed = model.prefill(torch.cat(seqs), cu)
+    torch.cuda.synchronize()
+    assert packed.shape == (len(lens), cfg.vocab_size) and bool(torch.isfinite(packed).all())
+    for i, s in enumerate(seqs):
+        alone = model.prefill(s)[0]
+        cs = torch.nn.functional.cosine_similarity(packed[i].double(), alone.double(), dim=0)
+        assert float(cs) > 0.999, (i, float(cs))

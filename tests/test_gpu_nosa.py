@@ -181,6 +181,15 @@ def test_nosa_select_tied_cis_scores():
 # ---------------------------------------------------------------------------
 # CIS-biased attention
 # ---------------------------------------------------------------------------
+def test_nosa_select_batch_without_any_compressed_key():
+    """No compressed key in the whole batch: the plans are the forced pages only."""
+    lens = (20, 3, 31)
+    case = workloads.hidden_space_layer(lens, device=DEV, seed=21)
+    cis = _cis(sum(lens), 2, seed=21)
+    _check_nosa_select(case, cis, list(range(sum(lens))), topk=8, init=1, local=2, select=2,
+                       min_exact=1.0)
+
+
 def _check_nosa_attention(case, cis, ids, rows, **kw):
     out, lse = nosa_sparse_attention(case.q, case.k, case.v, cis.to(DEV), case.cu_seqlens,
                                      case.cu_seqlens, case.max_seqlen, case.max_seqlen, ids,

@@ -80,6 +80,23 @@ def test_select_ragged_with_short_sequences():
             assert bool((ids[:, cu[b] : cu[b + 1]] == -1).all())
 
 
+def test_batch_without_any_compressed_key():
+    """Every sequence shorter than one compression window: no compressed key in the
+    whole batch, so no page for any row (the reference skips such sequences,
+    minicpm.py:3115-3116) and a zero attention output."""
+    lens = (8, 31, 1)
+    case = workloads.hidden_space_layer(lens, device=DEV, seed=4)
+    kc, cu_c, ids = _select(case)
+    assert kc.shape[0] == 0 and cu_c.cpu().tolist() == [0, 0, 0, 0]
+    assert ids.shape == (2, sum(lens), 1) and bool((ids == -1).all())
+    out, ids2 = leanselect_sparse_prefill(
+        case.q, case.k, case.v, case.cu_seqlens, case.selector, topk=case.topk,
+        local_blocks=case.local_blocks, init_blocks=case.init_blocks,
+        cu_seqlens_host=case.cu_host, return_topk_idx=True)
+    torch.cuda.synchronize()
+    assert torch.equal(ids2, ids) and not bool(out.any())
+
+
 def test_select_32k_sampled_rows():
     case = workloads.hidden_space_layer((32768,), device=DEV, seed=3)
     rows = spread_rows(case.cu_host, per_seq=128)

@@ -137,3 +137,16 @@ def test_q_idx_is_aligned_to_the_longest_sequence():
     assert q[:4].tolist() == [0, 0, 0, 1]          # (t + 61) // 64
     assert q[69].item() == (69 + 61) // 64 == 2
     assert q[70:72].tolist() == [0, 0] and q[-1].item() == 130 // 64
+
+
+def test_page_maxpool_of_zero_width_scores_is_the_forced_overlay():
+    """No score column at all (every sequence shorter than a CIS window): every page
+    pools an empty range (-inf) and only the forced pages remain (+inf)."""
+    cu = torch.tensor([0, 20, 23, 54])
+    out = oracle.page_maxpool_varlen(torch.zeros(2, 54, 0), cu, cu, torch.zeros(3, dtype=torch.int32),
+                                     31, 31, local_blocks=2, init_blocks=1)
+    assert out.shape == (2, 54, 1)
+    assert bool(torch.isposinf(out).all())  # page 0 is the sink page of every row
+    out = oracle.page_maxpool_varlen(torch.zeros(1, 54, 0), cu, cu, torch.zeros(3, dtype=torch.int32),
+                                     31, 31, local_blocks=0, init_blocks=0)
+    assert bool(torch.isposinf(out).all())  # page 0 is each row's own local page
