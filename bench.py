@@ -92,6 +92,8 @@ def selection_flops(case, D: int = 128, F: int = 128, all_pages: bool = False) -
             atom_dots += n * A
             continue
         for qb in range((n + 63) // 64):
+            if qb - case.local_blocks - 1 < case.init_blocks:
+                continue  # no non-forced visible page yet
             hi = min(4 * (qb - case.local_blocks) - 1, A - 1)  # last atom of page qb-local-1
             lo = max(4 * case.init_blocks - 1, 0)
             rows = min(64, n - 64 * qb)
