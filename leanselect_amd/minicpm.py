@@ -92,6 +92,15 @@ def _rows(t: torch.Tensor, name: str) -> torch.Tensor:
     return t
 
 
+def _out(out: torch.Tensor, shape: tuple, like: torch.Tensor) -> torch.Tensor:
+    """A caller-given output must have exactly the output's shape, dtype and device."""
+    _rows(out, "out")
+    if tuple(out.shape) != tuple(shape) or out.dtype != like.dtype or out.device != like.device:
+        raise ValueError(f"out must be {tuple(shape)} {like.dtype} on {like.device}, "
+                         f"got {tuple(out.shape)} {out.dtype} on {out.device}")
+    return out
+
+
 def rotary_tables(head_dim: int, max_pos: int, base: float, device) -> tuple[torch.Tensor, torch.Tensor]:
     """float32 ``(cos, sin)`` ``[max_pos, head_dim]`` built like
     ``MiniCPMRotaryEmbedding._set_cos_sin_cache`` (minicpm.py:804-838)."""
@@ -109,7 +118,8 @@ def rms_layernorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     n, hidden = x.shape
     if weight.shape != (hidden,) or weight.dtype != x.dtype:
         raise ValueError("weight must be [hidden] in x's dtype")
-    out = torch.empty_like(x, memory_format=torch.contiguous_format) if out is None else _rows(out, "out")
+    out = (torch.empty((n, hidden), dtype=x.dtype, device=dev) if out is None
+           else _out(out, (n, hidden), x))
     _hip.check(_hip.lib().ls_rmsnorm(
         x.data_ptr(), x.stride(0), weight.contiguous().data_ptr(), n, hidden, float(eps),
         _hip.dtype_code(x.dtype), out.data_ptr(), out.stride(0), _hip.stream_of(dev)), "ls_rmsnorm")
@@ -129,7 +139,8 @@ def add_rms_layernorm(residual: torch.Tensor, h: torch.Tensor, h_scale: float,
         raise ValueError("h must match residual's shape and dtype")
     if weight.shape != (hidden,) or weight.dtype != residual.dtype:
         raise ValueError("weight must be [hidden] in residual's dtype")
-    out = torch.empty((n, hidden), dtype=residual.dtype, device=dev) if out is None else _rows(out, "out")
+    out = (torch.empty((n, hidden), dtype=residual.dtype, device=dev) if out is None
+           else _out(out, (n, hidden), residual))
     _hip.check(_hip.lib().ls_add_rmsnorm(
         residual.data_ptr(), residual.stride(0), h.data_ptr(), h.stride(0), float(h_scale),
         weight.contiguous().data_ptr(), n, hidden, float(eps), _hip.dtype_code(residual.dtype),
@@ -150,6 +161,8 @@ def rope_inplace(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, si
     if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape \
             or cos.ndim != 2 or cos.shape[1] != head_dim:
         raise ValueError("cos/sin must be float32 [table_rows, head_dim]")
+    if x.shape[1] < max(n_q_heads * head_dim, k_col_offset + n_k_heads * head_dim):
+        raise ValueError("the query and key heads must lie inside x's columns")
     if check_positions and positions.numel():
         lo, hi = int(positions.min()), int(positions.max())
         if lo < 0 or hi >= cos.shape[0]:
@@ -168,7 +181,8 @@ def silu_mul(gate_up: torch.Tensor, inter: int, out: torch.Tensor | None = None)
     n = gate_up.shape[0]
     if gate_up.shape[1] < 2 * inter:
         raise ValueError("gate_up must hold 2*inter columns")
-    out = torch.empty((n, inter), dtype=gate_up.dtype, device=dev) if out is None else _rows(out, "out")
+    out = (torch.empty((n, inter), dtype=gate_up.dtype, device=dev) if out is None
+           else _out(out, (n, inter), gate_up))
     _hip.check(_hip.lib().ls_silu_mul(
         gate_up.data_ptr(), gate_up.stride(0), n, inter, _hip.dtype_code(gate_up.dtype),
         out.data_ptr(), out.stride(0), _hip.stream_of(dev)), "ls_silu_mul")

@@ -150,3 +150,27 @@ def test_model_wrappers_refuse_cpu_tensors():
         minicpm.silu_mul(torch.zeros(4, 128, dtype=torch.bfloat16), 64)
     with pytest.raises(RuntimeError, match="GPU"):
         minicpm.MiniCPMLeanSelect(minicpm.MiniCPMConfig(num_hidden_layers=1), device="cpu")
+
+
+def test_model_wrappers_check_outputs_and_views_before_any_launch(monkeypatch):
+    """Shape checks run before the GPU is touched (the device check is bypassed here
+    so the host-side validation is what raises)."""
+    from leanselect_amd import _hip as hip
+    from leanselect_amd import minicpm
+
+    monkeypatch.setattr(hip, "require_gpu", lambda *t: t[0].device)
+    monkeypatch.setattr(hip, "lib", lambda: (_ for _ in ()).throw(AssertionError("launched")))
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    w = torch.ones(64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="out must be"):
+        minicpm.rms_layernorm(x, w, 1e-6, out=torch.zeros(3, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="out must be"):
+        minicpm.add_rms_layernorm(x, x.clone(), 1.0, w, 1e-6, out=torch.zeros(4, 64))
+    with pytest.raises(ValueError, match="out must be"):
+        minicpm.silu_mul(torch.zeros(4, 128, dtype=torch.bfloat16), 64,
+                         out=torch.zeros(4, 32, dtype=torch.bfloat16))
+    qkv = torch.zeros(4, 4608, dtype=torch.bfloat16)
+    cos = torch.zeros(10, 128)
+    with pytest.raises(ValueError, match="inside"):
+        minicpm.rope_inplace(qkv[:, :4096], torch.zeros(4, dtype=torch.int32), cos, cos,
+                             n_q_heads=32, n_k_heads=2, k_col_offset=4096)
