@@ -96,6 +96,7 @@ __global__ void ls_attn_plan_kernel(const int32_t* __restrict__ cu_q,
 #define LS_ATT_KBYTES (64 * 256)             // K page: 64 rows x 256 B
 #define LS_ATT_STAGE_BYTES (2 * LS_ATT_KBYTES)  // + V^T page: 128 rows x 128 B
 #define LS_ATT_WORDS (LS_ATTN_MAX_PAGES / 32)
+#define LS_ATT_XCD_CHUNK 32                  // consecutive tiles per XCD run
 #define LS_ATT_MAX_UNION (LS_ATT_TILE * LS_ATTN_MAX_TAKE)
 
 typedef _Float16 ls_half2 __attribute__((ext_vector_type(2)));
@@ -243,9 +244,18 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, q = lane >> 4;
 
-  // XCD-aware tile order: consecutive workgroups land on different XCDs, so
-  // give each XCD a contiguous run of tiles (neighbouring rows share pages).
-  const int64_t tile = (int64_t)(LS_BID_X % 8) * per_xcd + LS_BID_X / 8;
+  // XCD-aware tile order.  Consecutive workgroups land on different XCDs
+  // (workgroup x runs on XCD x % 8).  Each XCD takes runs of LS_ATT_XCD_CHUNK
+  // consecutive tiles, so the tiles in flight on one XCD are neighbours that
+  // share pages in its L2, and the runs go round-robin over the XCDs, so every
+  // XCD gets an even share of early (small-union) and late (large-union) rows.
+  // Runs are taken from the end of the sequence first: the largest tiles
+  // start first and small ones fill the tail.  The grid is a multiple of
+  // 8 * LS_ATT_XCD_CHUNK, so this is a permutation of the workgroup indices.
+  const int64_t xi = LS_BID_X / 8;
+  const int64_t tile = 8LL * per_xcd - 1 -
+                       ((xi / LS_ATT_XCD_CHUNK) * (8 * LS_ATT_XCD_CHUNK) +
+                        (int64_t)(LS_BID_X % 8) * LS_ATT_XCD_CHUNK + xi % LS_ATT_XCD_CHUNK);
   if (tile >= tile_off[batch]) return;
   const int g = LS_BID_Y;
   const int head = LS_BID_Z * 16 + r;
@@ -772,7 +782,9 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf((float)head_dim);
   const float scale_log2 = scale * 1.4426950408889634f;
   const int64_t tile_bound = (total_q + LS_ATT_TILE - 1) / LS_ATT_TILE + batch;
-  const dim3 grid((unsigned)(8 * ((tile_bound + 7) / 8)), num_kv_heads, (gs + 15) / 16);
+  constexpr int64_t kRound = 8 * LS_ATT_XCD_CHUNK;  // whole runs on every XCD
+  const dim3 grid((unsigned)(kRound * ((tile_bound + kRound - 1) / kRound)), num_kv_heads,
+                  (gs + 15) / 16);
 #define LS_TILE_ARGS                                                                              \
   grid, s, q, q_row_stride, kv, L, vexp, cb, tok, cu_seqlens_q, cu_seqlens_k, pg,              \
       tiles, batch, total_q, num_kv_heads, gs, topk_idx, take, scale_log2, causal, out, lse
