@@ -170,6 +170,14 @@ def test_attention_ragged_batch():
     assert bool((out[:32] == 0).all())
 
 
+def test_attention_every_row_of_a_ragged_batch():
+    """Every row of a batch whose tile count (16-row tiles per sequence) is far from a
+    multiple of the launch's rounding: each tile index reaches exactly one workgroup
+    of the XCD-dealt grid, and surplus workgroups exit without writing."""
+    case, ids = _attention_case(lens=(700, 1300, 64, 17, 2500, 333), seed=8)
+    _check_attention(case, ids, list(range(case.cu_host[-1])))
+
+
 def test_attention_messy_ids_duplicates_unsorted_out_of_range():
     case, ids = _attention_case(lens=(1500,), seed=7)
     g = torch.Generator(device="cpu").manual_seed(0)
