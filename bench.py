@@ -2,7 +2,8 @@
 
 One step = one MiniCPM4.1-8B attention layer of LeanSelect sparse prefill on a
 128K-token sequence (bf16, 32 query / 2 KV heads, head_dim 128, page 64,
-budget 64 pages = 1 sink + 4 local + 59 selected): compressed keys, page
+budget 64 pages = 1 sink + 5 local (4 local blocks and the query's own page)
++ 58 selected): compressed keys, page
 selection and block-sparse attention, with inputs resident in HBM.
 
 Prints one JSON line (metric: ms per layer, lower is better) with a roofline
@@ -77,6 +78,29 @@ def attention_keys(ids: torch.Tensor, cu_host: list[int]) -> int:
     return int((keys * valid).sum())
 
 
+def plan_locality(ids: torch.Tensor, cu_host: list[int], tile: int = 16) -> dict:
+    """Mean distinct pages of a ``tile``-row query tile's plans (per KV group), and
+    the mean number of the tile's rows that chose each of those pages: how much
+    K/V one staged page serves."""
+    G, N, T = ids.shape
+    unions, chosen = 0.0, 0.0
+    n_tiles = 0
+    for b in range(len(cu_host) - 1):
+        s, e = cu_host[b], cu_host[b + 1]
+        n = (e - s) // tile
+        if n == 0:
+            continue
+        x = ids[:, s : s + n * tile].reshape(G, n, tile * T)
+        xs = x.sort(-1).values
+        first = torch.ones_like(xs[..., :1], dtype=torch.bool)
+        distinct = (xs >= 0) & torch.cat([first, xs[..., 1:] != xs[..., :-1]], -1)
+        unions += float(distinct.sum())
+        chosen += float((xs >= 0).sum())
+        n_tiles += G * n
+    return {"tile_rows": tile, "union_pages_per_tile": round(unions / max(n_tiles, 1), 1),
+            "rows_per_union_page": round(chosen / max(unions, 1.0), 2)}
+
+
 def selection_flops(case, D: int = 128, F: int = 128, all_pages: bool = False) -> float:
     """q~ projection + k~ projection + the atom dots of the non-forced visible pages
     (of every page with atoms when ``all_pages``: the NOSA shortlist ranks them all)."""
@@ -120,42 +144,74 @@ def _event_ms(fn, iters: int) -> float:
     return start.elapsed_time(end) / iters
 
 
-def cpu_baseline(case, rows_per_seq: int, threads: int) -> dict:
-    """The CPU oracle on a row sample, scaled to ms per layer."""
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_s(fn, runs: int, cap_s: float) -> tuple[float, int]:
+    """Median wall time of ``runs`` calls (fewer when one call exceeds ``cap_s``)."""
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if times[-1] > cap_s:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline(case, attn_rows: int, threads: int, runs: int = 3) -> dict:
+    """The reference's torch formulation of the path on the host CPU, ms per layer.
+
+    Compressed keys and the whole selection (every query row) run in the
+    activation dtype as the reference runs them (einsums, max_pool1d,
+    torch.topk); attention is a gather-based float32 masked softmax timed on an
+    even sample of query rows and scaled to the layer.  Each part is the median
+    of ``runs`` warm runs.
+    """
     import oracle
 
     torch.set_num_threads(threads)
     q, k, v = case.q.cpu(), case.k.cpu(), case.v.cpu()
     cu = case.cu_host
-    rows = []
-    for b in range(len(cu) - 1):
-        n = cu[b + 1] - cu[b]
-        step = max(1, n // rows_per_seq)
-        rows += list(range(cu[b] + step - 1, cu[b + 1], step))
-    sel = case.selector
-    t0 = time.perf_counter()
-    kc, cu_c = oracle.compress_k(k, cu)
-    qf, kf = oracle.fused_weights(sel.head_mix.cpu(), sel.kv_head_mix.cpu(), sel.q_proj.cpu(),
-                                  sel.k_proj.cpu(), q.dtype)
-    t1 = time.perf_counter()
-    ids = oracle.select_prefill(q, kc, cu, cu_c.tolist(), qf, kf, topk=case.topk,
-                                init_blocks=case.init_blocks, local_blocks=case.local_blocks,
-                                rows=rows)
-    t2 = time.perf_counter()
-    oracle.sparse_attention(q, k, v, cu, cu, ids, rows=rows, ids_rows_aligned=True)
-    t3 = time.perf_counter()
     N = cu[-1]
+    sel = case.selector
+    masters = [getattr(sel, n).detach().float().cpu()
+               for n in ("head_mix", "kv_head_mix", "q_proj", "k_proj")]
+    kw = dict(topk=case.topk, init_blocks=case.init_blocks, local_blocks=case.local_blocks)
+    kc, cu_c = oracle.reference_compress_k(k, cu)  # warm-up, and the selection's input
+    ids = oracle.reference_select_prefill(q, kc, cu, cu_c, masters, **kw)
+    step = max(1, N // attn_rows)
+    rows = list(range(step // 2, N, step))
+    oracle.reference_sparse_attention_rows(q, k, v, cu, ids, rows[:64])
+    t_c, n_c = _median_s(lambda: oracle.reference_compress_k(k, cu), runs, 60.0)
+    t_s, n_s = _median_s(lambda: oracle.reference_select_prefill(q, kc, cu, cu_c, masters, **kw),
+                         runs, 60.0)
+    t_a, n_a = _median_s(lambda: oracle.reference_sparse_attention_rows(q, k, v, cu, ids, rows),
+                         runs, 60.0)
     scale = N / len(rows)
-    ms = 1e3 * ((t1 - t0) + (t2 - t1) * scale + (t3 - t2) * scale)
+    ms = 1e3 * (t_c + t_s + t_a * scale)
     return {
         "value": round(ms, 1),
         "unit": "ms/layer",
         "cores": threads,
         "kind": "port",
-        "sample": (f"CPU oracle (float64 torch restatement) on {len(rows)} of {N} query rows "
-                   f"spread evenly per sequence: compressed keys in full ({1e3*(t1-t0):.0f} ms), "
-                   f"selection {1e3*(t2-t1):.0f} ms and attention {1e3*(t3-t2):.0f} ms for the "
-                   f"sample, both scaled by {scale:.1f}"),
+        "cpu_model": _cpu_model(),
+        "stages_ms": {"compress_k": round(1e3 * t_c, 1), "select": round(1e3 * t_s, 1),
+                      "sparse_attention": round(1e3 * t_a * scale, 1)},
+        "sample": (f"the reference's torch formulation on the host CPU ({threads} threads), "
+                   f"median of {min(n_c, n_s, n_a)}-{max(n_c, n_s, n_a)} warm runs: compressed "
+                   f"keys and selection of all {N} query rows in {str(q.dtype).split('.')[-1]} "
+                   f"(einsums, max_pool1d, torch.topk), attention (gather-based float32 masked "
+                   f"softmax) on {len(rows)} evenly spaced rows ({1e3 * t_a:.0f} ms) scaled by "
+                   f"{scale:.1f}"),
     }
 
 
@@ -269,8 +325,11 @@ def main() -> None:
     ap.add_argument("--workload", default="minicpm41_8b_layer_128k", choices=sorted(WORKLOADS))
     ap.add_argument("--variant", default="leanselect", choices=("leanselect", "nosa"))
     ap.add_argument("--kernel-iters", type=int, default=5)
-    ap.add_argument("--cpu-rows-per-seq", type=int, default=4096)
+    ap.add_argument("--cpu-attn-rows", type=int, default=1024,
+                    help="query rows of the CPU baseline's attention sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the secondary attention timing on plans without planted topics")
     ap.add_argument("--budget-pages", type=int, default=None,
                     help="model prefill only: total page budget (default 64)")
     ap.add_argument("--local-blocks", type=int, default=None,
@@ -352,6 +411,27 @@ def main() -> None:
     ms_attn = _event_ms(lambda: attend(ids), it)
 
     H, G, D = case.q.shape[1], case.k.shape[1], case.q.shape[2]
+    locality = plan_locality(ids, cu_host)
+    secondary_plans = None
+    if not nosa and not args.no_secondary:
+        # The same layer on hidden states without planted topics: plans that
+        # share few pages between neighbouring rows, like the whole-model
+        # prefill's on random token ids.
+        print("[bench] secondary: attention on plans without planted topics ...",
+              file=sys.stderr, flush=True)
+        c0 = workloads.hidden_space_layer(wl["seq_lens"], device=dev, seed=0, topic_amp=0.0)
+        kc0, cu_c0 = compress_k(c0.k, cu, cu_seqlens_host=cu_host)
+        ids0 = leanselect_prefill_topk_idx(c0.q, kc0, cu, cu_c0, c0.selector, **kw)
+        ms0 = _event_ms(lambda: sparse_attention(c0.q, c0.k, c0.v, cu, cu, max_len, max_len, ids0), it)
+        fl0 = 4.0 * (H // G) * D * attention_keys(ids0, cu_host)
+        secondary_plans = {
+            "data": "same shapes and seed, no planted topics (topic amplitude 0)",
+            "attention_ms": round(ms0, 4),
+            "attention_tflops": round(fl0 / (ms0 * 1e-3) / 1e12, 2),
+            "frac": round(fl0 / (ms0 * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "plan_locality": plan_locality(ids0, cu_host),
+        }
+        del c0, kc0, ids0
     n_keys = attention_keys(ids, cu_host)
     attn_flops = 4.0 * (H // G) * D * n_keys
     sel_flops = selection_flops(case, all_pages=nosa)
@@ -369,7 +449,12 @@ def main() -> None:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded hidden states with planted rank-8 page topics, random-init projections)",
+        "data": ("synthetic: seeded hidden states X ~ N(0,1) [N, 4096] with rank-8 page topics "
+                 "planted at amplitude 48 (each 64-token query block and 8 of its earlier pages "
+                 "share a topic direction; the amplitude is this benchmark's choice, the "
+                 "reference fixes none), random-init projections (std 0.02); plan locality "
+                 "in config.plan_locality, and secondary.attention_without_topics for plans "
+                 "that share few pages"),
         "config": {
             "workload": args.workload,
             "seq_lens": list(wl["seq_lens"]),
@@ -378,6 +463,7 @@ def main() -> None:
             "local_blocks": case.local_blocks, "router": "4x32",
             **({"variant": "nosa", "select_blocks": 24, "cis": "bf16 N(0,1)"} if nosa else {}),
             "parallelism": "single-gpu",
+            "plan_locality": locality,
         },
         "stages_ms": {"compress_k": round(ms_compress, 4), "select": round(ms_select, 4),
                       "sparse_attention": round(ms_attn, 4)},
@@ -396,12 +482,16 @@ def main() -> None:
         "secondary": {
             "select_tflops": round(sel_flops / (ms_select * 1e-3) / 1e12, 2),
             "select_flops": sel_flops,
+            "attention_without_topics": secondary_plans,
         },
     }
     if not args.no_cpu_baseline and not nosa:
+        # The host cores of this GPU's share (OMP_NUM_THREADS on a shared box).
         threads = len(os.sched_getaffinity(0))
+        if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+            threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
         print(f"[bench] CPU baseline on {threads} threads ...", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(case, args.cpu_rows_per_seq, threads)
+        result["cpu_baseline"] = cpu_baseline(case, args.cpu_attn_rows, threads)
     print(json.dumps(result), flush=True)
 
 

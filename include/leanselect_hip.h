@@ -25,6 +25,8 @@ extern "C" {
 
 enum { LS_F32 = 0, LS_BF16 = 1, LS_F16 = 2 };
 
+enum { LS_ATTN_RING_TIMEOUT = 1 };
+
 enum {
   LS_OK = 0,
   LS_ERR_INVALID = 1,     /* bad shape, geometry or pointer */
@@ -166,6 +168,13 @@ int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t total_q, cons
 
 /*
  * Workspace bytes needed by ls_sparse_attn_varlen.
+ *
+ * Status word: the first 4 bytes of an attention workspace (this entry point's
+ * and ls_nosa_attn_varlen's) hold an int32 status once the call's kernels have
+ * completed on `stream`: 0, or LS_ATTN_RING_TIMEOUT when a wave's bounded wait
+ * for a staged page expired, in which case the outputs are invalid.  The
+ * kernels never synchronise; a caller reads the word after the stream work
+ * ends (the Python mirror does so after every call and raises RuntimeError).
  */
 size_t ls_sparse_attn_workspace_size(int64_t total_k, int32_t batch, int32_t num_kv_heads,
                                      int32_t head_dim, int32_t max_seqlen_k, int32_t dtype);
@@ -193,6 +202,17 @@ int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const void* k,
                           int32_t take, int32_t block_size, float softmax_scale,
                           int32_t causal, void* out, float* lse, void* workspace,
                           size_t workspace_bytes, void* stream);
+
+/*
+ * Bound of one wait of the attention kernels for a staged page, in polls
+ * (default 1 << 22, far above any wait of a working launch).  Sets the bound
+ * for later launches from this process and returns the previous one; a
+ * negative value restores the default.  A testing hook: a bound of 0 makes
+ * every wait expire at once (the kernels still finish, with the status word
+ * set), so the error path can be exercised without a fault.  No counterpart in
+ * the reference.
+ */
+int32_t ls_attn_set_spin_limit(int32_t spins);
 
 /* ------------------------------------------------------------------------ */
 /* NOSA variant (leanselect/models/nosa.py, --method leanselect)             */

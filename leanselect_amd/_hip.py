@@ -14,6 +14,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libleanselect_hip.so")
 
 LS_F32, LS_BF16, LS_F16 = 0, 1, 2
 LS_OK, LS_ERR_INVALID, LS_ERR_UNSUPPORTED, LS_ERR_WORKSPACE, LS_ERR_HIP = range(5)
+LS_ATTN_RING_TIMEOUT = 1
 
 _i32, _i64, _f32, _sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 _p = ctypes.c_void_p
@@ -41,6 +42,7 @@ SIGNATURES = {
         _i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p,
                _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i32, _p, _sz, _p]),
     "ls_sparse_attn_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32]),
+    "ls_attn_set_spin_limit": (_i32, [_i32]),
     "ls_sparse_attn_varlen": (
         _i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _i32, _i64, _i64, _i32, _i32, _i32, _i32,
                _i32, _i32, _p, _i32, _i32, _f32, _i32, _p, _p, _p, _sz, _p]),
@@ -124,6 +126,40 @@ def require_gpu(*tensors: torch.Tensor) -> torch.device:
     if dev is None:
         raise ValueError("no tensor argument")
     return dev
+
+
+def check_cu_seqlens(cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor) -> None:
+    """Both prefix-offset arrays must be 1-D int32 of the same length (the kernels
+    read them as int32 ``[batch + 1]``)."""
+    for name, t in (("cu_seqlens_q", cu_seqlens_q), ("cu_seqlens_k", cu_seqlens_k)):
+        if t.dtype != torch.int32 or t.ndim != 1 or t.numel() < 1:
+            raise ValueError(f"{name} must be a 1-D int32 tensor of batch + 1 offsets, "
+                             f"got {t.dtype} {tuple(t.shape)}")
+    if cu_seqlens_q.numel() != cu_seqlens_k.numel():
+        raise ValueError(f"cu_seqlens_q and cu_seqlens_k differ in length "
+                         f"({cu_seqlens_q.numel()} != {cu_seqlens_k.numel()})")
+
+
+def check_out(out: torch.Tensor, shape: tuple, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """A caller-given output must be contiguous with exactly the output's shape,
+    dtype and device (the kernels write it densely)."""
+    if (tuple(out.shape) != tuple(shape) or out.dtype != dtype or out.device != device
+            or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous {tuple(shape)} {dtype} tensor on {device}, "
+                         f"got {tuple(out.shape)} {out.dtype} on {out.device}"
+                         f"{'' if out.is_contiguous() else ' (not contiguous)'}")
+    return out
+
+
+def check_attn_status(ws: torch.Tensor, name: str) -> None:
+    """Read an attention workspace's status word (its first 4 bytes) once the
+    call's kernels have finished, and raise if a wave's wait for a staged page
+    expired.  This waits for the stream."""
+    status = int(ws[:4].view(torch.int32).item())
+    if status & LS_ATTN_RING_TIMEOUT:
+        raise RuntimeError(f"{name}: a wait for a staged K/V page expired; the output is invalid")
+    if status:
+        raise RuntimeError(f"{name}: unknown status {status:#x}")
 
 
 def stream_of(device: torch.device) -> int:

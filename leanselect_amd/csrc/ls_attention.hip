@@ -32,6 +32,7 @@
 
 #define LS_ATTN_MAX_PAGES 8192
 #define LS_ATTN_MAX_TAKE 128
+#define LS_ATTN_RING_TIMEOUT 1  // status bit: a ring wait expired (outputs invalid)
 
 __device__ __forceinline__ void ls_wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -53,14 +54,17 @@ __device__ __forceinline__ int ls_wave_excl_scan(int v, int lane, int* total) {
 // pg_off[b] = sum_{b' < b} ceil(len_k(b') / 64): page-aligned start of each
 // sequence in the transposed V copy (in pages); tile_off[b] = sum_{b' < b}
 // ceil(len_q(b') / tile): first row tile of each sequence; tok[i] = i for
-// i < n_tok (the ready tokens the tile kernel's copies deliver).
+// i < n_tok (the ready tokens the tile kernel's copies deliver); *status = 0
+// (the tile kernel ORs in LS_ATTN_RING_TIMEOUT when a ring wait expires).
 __global__ void ls_attn_plan_kernel(const int32_t* __restrict__ cu_q,
                                     const int32_t* __restrict__ cu_k, int batch, int tile,
                                     int32_t* __restrict__ pg_off, int32_t* __restrict__ tile_off,
-                                    int32_t* __restrict__ tok, int n_tok) {
+                                    int32_t* __restrict__ tok, int n_tok,
+                                    int32_t* __restrict__ status) {
   if (LS_BID_X != 0) return;
   for (int i = LS_TID; i < n_tok; i += 64) tok[i] = i;
   if (LS_TID != 0) return;
+  *status = 0;
   int32_t acc = 0, acc_t = 0;
   pg_off[0] = 0;
   tile_off[0] = 0;
@@ -211,7 +215,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     const int32_t* __restrict__ pg_off, const int32_t* __restrict__ tile_off, int batch,
     int64_t total_q, int G, int gs, const int32_t* __restrict__ topk_idx, int take,
     float scale_log2, int causal, uint16_t* __restrict__ out, float* __restrict__ lse,
-    int per_xcd) {
+    int per_xcd, int32_t* __restrict__ status, int spin_limit) {
   constexpr int D = 128;
   constexpr uint32_t ROWS_MASK = LS_ATT_TPW == 32 ? 0xffffffffu : ((1u << LS_ATT_TPW) - 1u);
   // The per-row page bitmaps are only needed before streaming starts and
@@ -605,12 +609,20 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     uint64_t sw = stage_word(ui);
     if (!is_ready(ui, sw)) {
       // Bounded wait (the protocol cannot deadlock; the bound only guarantees
-      // that a wave always finishes).
-      for (int spin = 0; spin < (1 << 22); ++spin) {
+      // that a wave always finishes).  A wave whose wait expires reports it
+      // in the status word and goes on; the host turns that into an error.
+      bool landed = false;
+      for (int spin = 0; spin < spin_limit; ++spin) {
         if (!try_claim(ui)) __builtin_amdgcn_s_sleep(1);
         sw = stage_word(ui);
-        if (is_ready(ui, sw)) break;
+        if (is_ready(ui, sw)) {
+          landed = true;
+          break;
+        }
       }
+      if (!landed && lane == 0)
+        __hip_atomic_fetch_or(status, LS_ATTN_RING_TIMEOUT, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
     }
 
     const int nxt = next_page(ui);
@@ -673,8 +685,11 @@ __global__ __launch_bounds__(64) void ls_bias_kernel(const typename LsElem<CT>::
 // Host side
 // ---------------------------------------------------------------------------
 namespace {
+constexpr int kDefaultSpinLimit = 1 << 22;
+int g_spin_limit = kDefaultSpinLimit;  // bound of one ring wait (in polls)
+
 struct AttnWs {
-  size_t kv, pg, tiles, vexp, cb, tok, total;
+  size_t status, kv, pg, tiles, vexp, cb, tok, total;
   int64_t lpad, n_pages;
 };
 AttnWs attn_ws(int64_t total_k, int batch, int G, bool bias) {
@@ -682,6 +697,7 @@ AttnWs attn_ws(int64_t total_k, int batch, int G, bool bias) {
   L.n_pages = (total_k + 63) / 64 + batch;
   L.lpad = L.n_pages * 64;
   size_t off = 0;
+  L.status = off; off += 256;  // the call's status word comes first
   L.kv = off; off += ls_align256((size_t)G * L.n_pages * LS_ATT_STAGE_BYTES);
   L.pg = off; off += ls_align256((size_t)(batch + 1) * 4);
   L.tiles = off; off += ls_align256((size_t)(batch + 1) * 4);
@@ -699,11 +715,12 @@ void launch_tile(dim3 grid, hipStream_t s, const void* q, int64_t q_rs, const ui
                  const int32_t* cu_q, const int32_t* cu_k, const int32_t* pg,
                  const int32_t* tiles, int batch, int64_t total_q, int G, int gs,
                  const int32_t* topk_idx, int take, float scale_log2, int causal, void* out,
-                 float* lse) {
+                 float* lse, int32_t* status) {
   hipLaunchKernelGGL((ls_attn_tile_kernel<DT, BIAS>), grid, dim3(LS_ATT_THREADS), 0, s,
                      (const uint16_t*)q, q_rs, kv, L.lpad, vexp, cb, tok,
                      L.n_pages, cu_q, cu_k, pg, tiles, batch, total_q, G, gs, topk_idx, take,
-                     scale_log2, causal, (uint16_t*)out, lse, (int)(grid.x / 8));
+                     scale_log2, causal, (uint16_t*)out, lse, (int)(grid.x / 8), status,
+                     g_spin_limit);
 }
 
 // Shared body of the plain and the NOSA (cis != nullptr) entry points.
@@ -750,8 +767,9 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   int32_t* tiles = (int32_t*)(ws + L.tiles);
   float* cb = bias ? (float*)(ws + L.cb) : nullptr;
   int32_t* tok = (int32_t*)(ws + L.tok);
+  int32_t* status = (int32_t*)(ws + L.status);
   hipLaunchKernelGGL(ls_attn_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens_q, cu_seqlens_k,
-                     batch, LS_ATT_TILE, pg, tiles, tok, LS_ATT_MAX_UNION + 1);
+                     batch, LS_ATT_TILE, pg, tiles, tok, LS_ATT_MAX_UNION + 1, status);
   int rc = ls_check_launch("ls_attn_plan_kernel");
   if (rc) return rc;
   if (total_k > 0) {
@@ -787,7 +805,8 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
                   (gs + 15) / 16);
 #define LS_TILE_ARGS                                                                              \
   grid, s, q, q_row_stride, kv, L, vexp, cb, tok, cu_seqlens_q, cu_seqlens_k, pg,              \
-      tiles, batch, total_q, num_kv_heads, gs, topk_idx, take, scale_log2, causal, out, lse
+      tiles, batch, total_q, num_kv_heads, gs, topk_idx, take, scale_log2, causal, out, lse, \
+      status
   if (dtype == LS_BF16) {
     if (bias) launch_tile<LS_BF16, true>(LS_TILE_ARGS);
     else launch_tile<LS_BF16, false>(LS_TILE_ARGS);
@@ -799,6 +818,12 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   return ls_check_launch("ls_attn_tile_kernel");
 }
 }  // namespace
+
+extern "C" int32_t ls_attn_set_spin_limit(int32_t spins) {
+  const int32_t prev = g_spin_limit;
+  g_spin_limit = spins < 0 ? kDefaultSpinLimit : spins;
+  return prev;
+}
 
 extern "C" size_t ls_sparse_attn_workspace_size(int64_t total_k, int32_t batch,
                                                 int32_t num_kv_heads, int32_t head_dim,

@@ -328,6 +328,10 @@ class MiniCPMLeanSelect:
         cu_host = list(cu_seqlens_host) if cu_seqlens_host is not None else [0, N]
         if cu_host[0] != 0 or cu_host[-1] != N or any(b < a for a, b in zip(cu_host, cu_host[1:])):
             raise ValueError("cu_seqlens_host must be non-decreasing from 0 to the token count")
+        if len(cu_host) < 2 or any(b == a for a, b in zip(cu_host, cu_host[1:])):
+            # Each sequence's logits are read at its last token, which an empty
+            # sequence does not have.
+            raise ValueError("every packed sequence must hold at least one token")
         dev = _hip.require_gpu(input_ids)
         cu = torch.tensor(cu_host, dtype=torch.int32, device=dev)
         pos = self.positions(cu_host, dev)

@@ -188,6 +188,10 @@ def nosa_sparse_attention(
         raise ValueError("q, k, v must be [tokens, heads, head_dim]")
     if topk_idx is None or topk_idx.ndim != 3:
         raise ValueError("topk_idx must be [num_kv_heads, total_q, k] int32")
+    # Host-side checks first: no launch may see int64 offsets or a misshapen output.
+    _hip.check_cu_seqlens(cu_seqlens_q, cu_seqlens_k)
+    if out is not None:
+        _hip.check_out(out, tuple(q.shape), q.dtype, q.device)
     dev = _hip.require_gpu(q, k, v, cis, cu_seqlens_q, cu_seqlens_k, topk_idx)
     total_q, H, D = q.shape
     total_k, G, Dk = k.shape
@@ -226,4 +230,5 @@ def nosa_sparse_attention(
         topk_idx.data_ptr(), topk_idx.shape[2], block_size, scale, out.data_ptr(),
         _hip.ptr(lse), ws.data_ptr(), ws.numel(), _hip.stream_of(dev))
     _hip.check(rc, "ls_nosa_attn_varlen")
+    _hip.check_attn_status(ws, "ls_nosa_attn_varlen")
     return (out, lse) if return_lse else out

@@ -408,8 +408,14 @@ def sparse_attention(
     block_size: int = 64,
     rows: Sequence[int] | None = None,
     ids_rows_aligned: bool = False,
+    return_abs: bool = False,
 ):
     """Reference outputs ``(out [R, H, D] in q.dtype, lse [H, R] float32)``.
+
+    With ``return_abs`` a third output ``[R, H, D]`` float64 holds
+    ``sum_j p_j |v_j|`` with the same softmax weights: the magnitude an output
+    element is summed from, which bounds the rounding error any 16-bit
+    evaluation of the weights can make when the terms cancel.
 
     ``O[t, h] = softmax_j(scale * Q[t, h] . K[j, h // gs]) V[j, h // gs]`` over
     the keys of ``attention_keys_for_row``; ``scale = head_dim ** -0.5`` when
@@ -427,23 +433,28 @@ def sparse_attention(
     scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
     row_list = list(range(total_q)) if rows is None else [int(r) for r in rows]
     out = torch.zeros((len(row_list), H, D), dtype=torch.float64)
+    mass = torch.zeros((len(row_list), H, D), dtype=torch.float64) if return_abs else None
     lse = torch.full((H, len(row_list)), float("inf"), dtype=torch.float64)
-    qd = q.detach().to(torch.float64)
-    kd = k.detach().to(torch.float64)
-    vd = v.detach().to(torch.float64)
+    # Only the rows and keys each output reads are widened to float64.
     for i, r in enumerate(row_list):
         for g in range(G):
             ids = topk_idx[g, i if ids_rows_aligned else r]
             keys = attention_keys_for_row(r, ids, cq, ck, block_size=block_size, causal=causal)
             if keys.numel() == 0:
                 continue
-            qh = qd[r, g * gs : (g + 1) * gs]  # [gs, D]
-            s = (qh @ kd[keys, g].T) * scale  # [gs, nk]
+            qh = q[r, g * gs : (g + 1) * gs].detach().to(torch.float64)  # [gs, D]
+            kk = k[keys, g].detach().to(torch.float64)
+            vv = v[keys, g].detach().to(torch.float64)
+            s = (qh @ kk.T) * scale  # [gs, nk]
             m = s.amax(dim=-1, keepdim=True)
             p = torch.exp(s - m)
             denom = p.sum(dim=-1, keepdim=True)
-            out[i, g * gs : (g + 1) * gs] = (p @ vd[keys, g]) / denom
+            out[i, g * gs : (g + 1) * gs] = (p @ vv) / denom
+            if mass is not None:
+                mass[i, g * gs : (g + 1) * gs] = (p @ vv.abs()) / denom
             lse[g * gs : (g + 1) * gs, i] = (m + torch.log(denom)).squeeze(-1)
+    if mass is not None:
+        return _round(out, q.dtype), lse.to(torch.float32), mass
     return _round(out, q.dtype), lse.to(torch.float32)
 
 

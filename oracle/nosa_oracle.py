@@ -39,6 +39,7 @@ from .leanselect_oracle import (
 
 __all__ = [
     "nosa_mean_pooling",
+    "nosa_window_means",
     "page_maxpool_varlen",
     "nosa_atom_scores",
     "nosa_q_idx",
@@ -74,6 +75,23 @@ def nosa_mean_pooling(cis_score: torch.Tensor, cu_seqlens, max_seqlen: int,
                 break
             val = c[s + m * stride : s + m * stride + kernel_size].mean(dim=0)  # [H]
             out[:, s:e, m] = val[:, None]
+    return _round(out, cis_score.dtype)
+
+
+def nosa_window_means(cis_score: torch.Tensor, start: int, end: int, max_seqlen: int,
+                      kernel_size: int = 32, stride: int = 16) -> torch.Tensor:
+    """``[H, M]``: the row vector ``nosa_mean_pooling`` broadcasts to every row of
+    the sequence ``[start, end)`` (the same float64 mean rounded once; 0 past the
+    sequence's last whole window)."""
+    N, H = cis_score.shape
+    M = max(int(max_seqlen) // stride - 1, 0)
+    out = torch.zeros((H, M), dtype=torch.float64)
+    n = end - start
+    n_win = min(M, (n - kernel_size) // stride + 1) if n >= kernel_size else 0
+    if n_win > 0:
+        c = cis_score[start:end].detach().to(torch.float64)
+        idx = torch.arange(n_win)[:, None] * stride + torch.arange(kernel_size)[None, :]
+        out[:, :n_win] = c[idx].mean(dim=1).T
     return _round(out, cis_score.dtype)
 
 
@@ -207,17 +225,24 @@ def nosa_select_prefill(
     R = len(row_list)
     G = atom_score.shape[0]
     s = block_size // kernel_stride
-    score_cis = nosa_mean_pooling(cis, cu_seqlens_k, max_seqlen_k, kernel_size, kernel_stride)
+    ck = _as_list(cu_seqlens_k)
+    # Row t of sequence b reads the b-th sequence's window means in the
+    # broadcast layout of nosa_mean_pooling; only those per-sequence vectors are
+    # formed here (the broadcast copy would be [G, total_q, M]).
+    means: dict[int, torch.Tensor] = {}
     out_len = (int(max_seqlen_q) + block_size - 1) // block_size
     block = torch.full((G, R, out_len), float("-inf"), dtype=torch.float64)
     block_cis = torch.full((G, R, out_len), float("-inf"), dtype=torch.float64)
     for i, r in enumerate(row_list):
         b = next(j for j in range(len(cq) - 1) if cq[j] <= r < cq[j + 1])
         lk = ckc[b + 1] - ckc[b]
+        if b not in means:
+            means[b] = nosa_window_means(cis, ck[b], ck[b + 1], max_seqlen_k, kernel_size,
+                                         kernel_stride)
         forced = _forced(torch.tensor([(r - cq[b]) // block_size]), out_len, init_blocks,
                          local_blocks)[0]
         pb = _pool_pages(atom_score[:, i].to(torch.float64), lk, out_len, s)
-        pc = _pool_pages(score_cis[:, r].to(torch.float64), lk, out_len, s)
+        pc = _pool_pages(means[b].to(torch.float64), lk, out_len, s)
         block[:, i] = pb.masked_fill(forced[None], float("inf"))
         block_cis[:, i] = pc.masked_fill(forced[None], float("inf"))
     q_idx_all = nosa_q_idx(cq, max_seqlen_q, block_size)
@@ -308,18 +333,18 @@ def nosa_attention(
     row_list = list(range(total_q)) if rows is None else [int(r) for r in rows]
     out = torch.zeros((len(row_list), H, D), dtype=torch.float64)
     lse = torch.full((H, len(row_list)), float("inf"), dtype=torch.float64)
-    qd, kd, vd = (x.detach().to(torch.float64) for x in (q, k, v))
-    cd = cis.detach().to(torch.float64)
+    f64 = torch.float64  # only the rows and keys each output reads are widened
     for i, r in enumerate(row_list):
         for g in range(G):
             ids = topk_idx[g, i if ids_rows_aligned else r]
             keys = attention_keys_for_row(r, ids, cq, ck, block_size=block_size, causal=True)
             if keys.numel() == 0:
                 continue
-            s = (qd[r, g * gs : (g + 1) * gs] @ kd[keys, g].T) * scale + cd[keys, g][None, :]
+            qh = q[r, g * gs : (g + 1) * gs].detach().to(f64)
+            s = (qh @ k[keys, g].detach().to(f64).T) * scale + cis[keys, g].detach().to(f64)[None, :]
             m = s.amax(dim=-1, keepdim=True)
             w = torch.exp(s - m)
-            out[i, g * gs : (g + 1) * gs] = (w @ vd[keys, g]) / w.sum(dim=-1, keepdim=True)
+            out[i, g * gs : (g + 1) * gs] = (w @ v[keys, g].detach().to(f64)) / w.sum(dim=-1, keepdim=True)
             lse[g * gs : (g + 1) * gs, i] = (m[:, 0] + torch.log(w.sum(dim=-1)))
     if return_lse:
         return _round(out, q.dtype), lse

@@ -11,13 +11,17 @@ repository is checked out; the tests read the fixtures.
 
 Usage: python tests/golden/make_selector_init.py [/path/to/LeanSelect]
 """
-import importlib.util
-import json
 import sys
-from pathlib import Path
 
-import torch
-from safetensors.torch import save_file
+# Executing the reference module must leave no bytecode beside its source.
+sys.dont_write_bytecode = True
+
+import importlib.util  # noqa: E402
+import json  # noqa: E402
+from pathlib import Path  # noqa: E402
+
+import torch  # noqa: E402
+from safetensors.torch import save_file  # noqa: E402
 
 CASES = [
     # name, num_heads, num_kv_heads, head_dim, router_heads, router_dim, seed

@@ -187,3 +187,13 @@ def test_variable_k_topk_mask_ties_to_lower_index():
     scores = torch.tensor([[1.0, 3.0, 3.0, float("-inf"), 2.0]])
     assert pages.variable_k_topk_mask(scores, 2).tolist() == [[False, True, True, False, False]]
     assert pages.variable_k_topk_mask(scores, 5).tolist() == [[True, True, True, False, True]]
+
+
+def test_attention_spin_limit_hook_is_host_only():
+    # Sets the bound for later launches and returns the previous one; no GPU call.
+    lib = _hip.lib()
+    default = lib.ls_attn_set_spin_limit(-1)
+    assert default == 1 << 22
+    assert lib.ls_attn_set_spin_limit(5) == default
+    assert lib.ls_attn_set_spin_limit(-1) == 5
+    assert lib.ls_attn_set_spin_limit(-1) == default

@@ -150,3 +150,73 @@ def test_page_maxpool_of_zero_width_scores_is_the_forced_overlay():
     out = oracle.page_maxpool_varlen(torch.zeros(1, 54, 0), cu, cu, torch.zeros(3, dtype=torch.int32),
                                      31, 31, local_blocks=0, init_blocks=0)
     assert bool(torch.isposinf(out).all())  # page 0 is each row's own local page
+
+
+def test_page_pooling_clips_to_each_sequence_and_the_choice_is_visible():
+    """The window of a row is clipped to its own sequence's score columns
+    (``cu_seqlens_k``), not to the padded width ``max_seqlen_k``.  The
+    reference's ``max_pooling_1d_varlen(input, cu_seqlens_q, cu_seqlens_k, ...,
+    max_seqlen_k, ...)`` (paper1.patch:2664-2760) receives the padded width
+    separately (it asserts ``input.shape[2] == max_seqlen_k``), so the per-sequence
+    offsets serve only to bound each sequence's columns.  Padding columns are
+    nonzero here, so the other clip gives a different answer and the check has
+    teeth."""
+    lens_q, lens_k = [300, 300], [9, 17]
+    cq, ck = _cu(lens_q), _cu(lens_k)
+    max_k = max(lens_k)
+    inp = torch.full((1, 600, max_k), -5.0, dtype=torch.float64)
+    inp[:, :300, 9:] = 7.0  # the first sequence's padding columns: larger than any score
+    got = oracle.page_maxpool_varlen(inp, cq, ck, torch.zeros(2, dtype=torch.int32), 300, max_k,
+                                     local_blocks=0, init_blocks=0)
+    out_len = (300 + 63) // 64
+    t = 299  # last row of sequence 0, page 4 (forced); pages 0..3 are pooled
+    own = _pool_loop(inp[0, t].tolist(), lens_k[0], out_len, 4, 0, 0)
+    padded = _pool_loop(inp[0, t].tolist(), max_k, out_len, 4, 0, 0)
+    assert got[0, t].tolist() == own
+    assert own != padded  # page 2 reads column 9 under the max_k clip
+    assert own[2] == -5.0 and padded[2] == 7.0 and own[3] == -math.inf
+
+
+def test_nosa_checker_flags_differences_without_a_tie():
+    # One row, out_len 8, q_idx 7: shortlist of 3 qk pages, then the 4 best CIS pages.
+    inf = math.inf
+    block = torch.tensor([[[inf, 5.0, 4.0, 3.0, 2.0, 1.0, 0.5, inf]]], dtype=torch.float64)
+    cis = torch.tensor([[[inf, 0.1, 0.2, 0.9, 0.8, 0.3, 0.7, inf]]], dtype=torch.float64)
+    q_idx = torch.tensor([7])
+    ids, b, over = oracle.nosa_two_stage(block, cis, q_idx, topk=4, qk_select=3,
+                                         return_scores=True)
+    assert ids.tolist() == [[[0, 1, 3, 7]]]  # shortlist {0, 7, 1}, then CIS 0.9 (page 3)
+    rep = oracle.check_nosa_topk(ids, ids, b, over, topk=4, qk_select=3)
+    assert rep.ok and rep.exact_rows == 1
+    wrong = torch.tensor([[[0, 1, 4, 7]]], dtype=torch.int32)  # 0.8 < 0.9: no tie
+    assert not oracle.check_nosa_topk(wrong, ids, b, over, topk=4, qk_select=3).ok
+    # A tie at the stage-2 boundary admits the other page.
+    cis_tie = cis.clone()
+    cis_tie[0, 0, 4] = 0.9
+    ids2, b2, over2 = oracle.nosa_two_stage(block, cis_tie, q_idx, topk=4, qk_select=3,
+                                            return_scores=True)
+    rep = oracle.check_nosa_topk(wrong, ids2, b2, over2, topk=4, qk_select=3)
+    assert rep.ok and rep.band_rows == 1
+    # A tie at the shortlist boundary (qk 4.0 vs 4.0) admits the other shortlist.
+    blk_tie = block.clone()
+    blk_tie[0, 0, 3] = 5.0
+    ids3, b3, over3 = oracle.nosa_two_stage(blk_tie, cis, q_idx, topk=4, qk_select=3,
+                                            return_scores=True)
+    other = torch.tensor([[[0, 3, 4, 7]]], dtype=torch.int32)
+    assert oracle.check_nosa_topk(other, ids3, b3, over3, topk=4, qk_select=3).ok
+    # A row with a different id count always fails.
+    short = torch.tensor([[[0, 1, 3, -1]]], dtype=torch.int32)
+    assert not oracle.check_nosa_topk(short, ids2, b2, over2, topk=4, qk_select=3).ok
+
+
+def test_window_means_are_the_broadcast_rows():
+    torch.manual_seed(5)
+    lens = [33, 100, 7, 400]
+    cu = _cu(lens)
+    cis = torch.randn(sum(lens), 2).to(torch.bfloat16)
+    full = oracle.nosa_mean_pooling(cis, cu, max(lens))
+    for b in range(len(lens)):
+        s, e = int(cu[b]), int(cu[b + 1])
+        row = oracle.nosa_window_means(cis, s, e, max(lens))
+        for t in range(s, e):
+            assert torch.equal(full[:, t], row)

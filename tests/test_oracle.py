@@ -300,12 +300,24 @@ def test_topk_checker_detects_planted_mistakes():
                              -math.inf]]], dtype=torch.float64)
     # take 4: forced {0, 6} + top-2 of {1: 5, 2: 1, 3: 4, 4: 4.0078, 5: .5}
     oracle_ids = torch.tensor([[[0, 1, 4, 6]]], dtype=torch.int32)
-    assert oracle.check_topk(oracle_ids, oracle_ids, scores, torch.float32).exact_rows == 1
-    # Page 3 vs 4 differ by less than one bf16 step: accepted in bf16 ...
+    rep = oracle.check_topk(oracle_ids, oracle_ids, scores, torch.float32)
+    assert rep.exact_rows == 1 and rep.band_rows == 0
+    # Pages 3 and 4 differ by 2**-9 relative, above the 1e-3 rule: a swap is a
+    # failure in every dtype (one bf16 step is no excuse).
     swap = torch.tensor([[[0, 1, 3, 6]]], dtype=torch.int32)
-    assert oracle.check_topk(swap, oracle_ids, scores, torch.bfloat16).ok
-    # ... but not under the plain float32 1e-3 rule (gap 2**-9 relative).
-    assert not oracle.check_topk(swap, oracle_ids, scores, torch.float32).ok
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        assert not oracle.check_topk(swap, oracle_ids, scores, dt).ok
+    # An exact tie at the boundary may go either way (counted as a band row).
+    tie = scores.clone()
+    tie[0, 0, 4] = 4.0
+    want = torch.tensor([[[0, 1, 3, 6]]], dtype=torch.int32)  # ties to the lower page
+    rep = oracle.check_topk(torch.tensor([[[0, 1, 4, 6]]], dtype=torch.int32), want, tie,
+                            torch.bfloat16)
+    assert rep.ok and rep.band_rows == 1 and rep.exact_rows == 0
+    # A near-tie inside 1e-3 relative is in the band too.
+    near = scores.clone()
+    near[0, 0, 4] = 4.0 * (1 + 5e-4)
+    assert oracle.check_topk(swap, oracle_ids, near, torch.float32).ok
     # A page far below the boundary, a missing forced page, an invisible page.
     for bad in ([0, 1, 2, 6], [0, 1, 3, 4], [0, 1, 4, 7], [0, 1, 1, 6]):
         rep = oracle.check_topk(torch.tensor([[bad]], dtype=torch.int32), oracle_ids, scores,
@@ -316,15 +328,59 @@ def test_topk_checker_detects_planted_mistakes():
 def test_attention_checker_tolerances():
     ref = torch.randn(64, 4, 128)
     ok, mx, mr = oracle.check_attention(ref + 1e-4, ref)
-    assert ok
+    assert ok and abs(mx - 1e-4) < 1e-6
     ok, _, _ = oracle.check_attention(ref + 3e-2, ref)
     assert not ok
-    # One bf16 step at |x| = 10 (0.0625) passes the magnitude-scaled max bound,
-    # eight steps do not.
+    # The raw 2e-2 bound applies wherever the output dtype resolves it ...
+    small = torch.full((1000,), 1.5)
+    off = small.clone()
+    off[0] += 0.03
+    assert not oracle.check_attention(off.to(torch.bfloat16), small)[0]
+    # ... and one bf16 step where a step is coarser (0.0625 at |x| = 10): two
+    # correct roundings can land on neighbouring values there; two steps cannot.
     ref = torch.full((1000,), 10.0)
     one = ref.clone()
     one[0] += 0.0625
-    ok, mx, _ = oracle.check_attention(one, ref)
-    assert ok and abs(mx - 0.00625) < 1e-9
-    one[0] += 0.4375
+    ok, mx, _ = oracle.check_attention(one.to(torch.bfloat16), ref)
+    assert ok and abs(mx - 0.0625) < 1e-9
+    two = ref.clone()
+    two[0] += 0.125
+    assert not oracle.check_attention(two.to(torch.bfloat16), ref)[0]
+    # float32 outputs get no step allowance.
     assert not oracle.check_attention(one, ref)[0]
+    # The mean bound: a uniform 2e-3 relative offset fails it.
+    assert not oracle.check_attention(ref * (1 + 2e-3), ref)[0]
+
+
+def test_output_step_matches_the_formats():
+    # Brute force through the format: the step at a representable x is the gap
+    # to the next representable value (the bit pattern plus one).
+    for dt in (torch.bfloat16, torch.float16):
+        x = torch.tensor([0.3, 1.0, 1.5, 3.9, 4.0, 10.0, -6.0]).to(dt)
+        bits = x.abs().view(torch.int16) + 1
+        gap = bits.view(dt).double() - x.abs().double()
+        assert torch.equal(oracle.output_step(x.double(), dt), gap), dt
+
+
+@pytest.mark.parametrize("init,local,block", [(1, 4, 64), (0, 0, 64), (3, 2, 16), (2, 32, 64)])
+def test_forced_page_mask_brute_force(init, local, block):
+    """``forced_page_mask`` (pages.py:222-240) against a per-element loop of its
+    contract: page p is forced for a query at absolute position t when p is a
+    sink page (p < init_blocks) or lies in the local window ending at the
+    query's page (qp - local_blocks <= p <= qp, qp = t // block_size); pages
+    after qp are never local.  Covers 1-D and batched 2-D positions."""
+    g = torch.Generator().manual_seed(init * 100 + local)
+    num_pages = 11
+    pos2 = torch.randint(0, num_pages * block, (3, 17), generator=g)
+    pos2[0, :4] = torch.tensor([0, block - 1, block, num_pages * block - 1])
+    for pos in (pos2[0], pos2):
+        got = oracle.forced_page_mask(pos, num_pages=num_pages, block_size=block,
+                                      init_blocks=init, local_blocks=local)
+        P = pos.view(1, -1) if pos.ndim == 1 else pos
+        assert got.shape == (P.shape[0], P.shape[1], num_pages)
+        for b in range(P.shape[0]):
+            for i in range(P.shape[1]):
+                qp = int(P[b, i]) // block
+                for p in range(num_pages):
+                    want = p < init or (qp - local <= p <= qp)
+                    assert bool(got[b, i, p]) == want, (b, i, p, qp)
