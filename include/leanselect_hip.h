@@ -204,6 +204,33 @@ int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const void* k,
                           size_t workspace_bytes, void* stream);
 
 /*
+ * Allocation-free ls_sparse_attn_varlen.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as ls_sparse_attn_varlen without the workspace: the
+ * kernels use a static device array of the library, LS_NOALLOC_SCRATCH_BYTES
+ * (64 MiB) per GPU, held from the library's first use of that GPU until the
+ * process ends.  The call allocates nothing (no hipMalloc / hipFree and no
+ * allocating library routine); a request whose workspace would exceed the
+ * array (ls_sparse_attn_workspace_size > 64 MiB, about 65000 keys at 2 KV
+ * heads) fails with LS_ERR_UNSUPPORTED before any device work.  `status`
+ * (optional, device int32) receives the status word described above; without
+ * it the word stays in the array.  Every call on one GPU shares that GPU's
+ * array, so calls that overlap on one GPU (concurrent streams or host threads)
+ * race and must be serialised by the caller.
+ */
+#define LS_NOALLOC_SCRATCH_BYTES (64u << 20)
+int ls_sparse_attn_varlen_noalloc(const void* q, int64_t q_row_stride, const void* k,
+                                  int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int32_t batch, int64_t total_q, int64_t total_k,
+                                  int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_heads,
+                                  int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                                  const int32_t* topk_idx, int32_t take, int32_t block_size,
+                                  float softmax_scale, int32_t causal, void* out, float* lse,
+                                  int32_t* status, void* stream);
+
+/*
  * Bound of one wait of the attention kernels for a staged page, in polls
  * (default 1 << 22, far above any wait of a working launch).  Sets the bound
  * for later launches from this process and returns the previous one; a

@@ -43,6 +43,9 @@ SIGNATURES = {
                _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i32, _p, _sz, _p]),
     "ls_sparse_attn_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32]),
     "ls_attn_set_spin_limit": (_i32, [_i32]),
+    "ls_sparse_attn_varlen_noalloc": (
+        _i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _i32, _i64, _i64, _i32, _i32, _i32, _i32,
+               _i32, _i32, _p, _i32, _i32, _f32, _i32, _p, _p, _p, _p]),
     "ls_sparse_attn_varlen": (
         _i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _i32, _i64, _i64, _i32, _i32, _i32, _i32,
                _i32, _i32, _p, _i32, _i32, _f32, _i32, _p, _p, _p, _sz, _p]),

@@ -22,6 +22,8 @@
 //     exact per-page power-of-two scale that moves onto P), output rounded once.
 #include "ls_common.h"
 
+#include <mutex>
+
 // Work-item and workgroup ids straight from the hardware: this file is built
 // without IEEE NaN quieting, and the device library's id helpers (built with
 // it) would then stay out-of-line calls.
@@ -731,7 +733,7 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
              int32_t max_seqlen_k, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
              int32_t dtype, const int32_t* topk_idx, int32_t take, int32_t block_size,
              float softmax_scale, int32_t causal, void* out, float* lse, void* workspace,
-             size_t workspace_bytes, void* stream) {
+             size_t workspace_bytes, void* stream, int32_t* status_out = nullptr) {
   const bool bias = cis != nullptr;
   LS_REQUIRE(dtype == LS_BF16 || dtype == LS_F16, LS_ERR_UNSUPPORTED,
              "%s: only bf16 and fp16 are supported (dtype %d)", who, dtype);
@@ -767,7 +769,7 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   int32_t* tiles = (int32_t*)(ws + L.tiles);
   float* cb = bias ? (float*)(ws + L.cb) : nullptr;
   int32_t* tok = (int32_t*)(ws + L.tok);
-  int32_t* status = (int32_t*)(ws + L.status);
+  int32_t* status = status_out ? status_out : (int32_t*)(ws + L.status);
   hipLaunchKernelGGL(ls_attn_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens_q, cu_seqlens_k,
                      batch, LS_ATT_TILE, pg, tiles, tok, LS_ATT_MAX_UNION + 1, status);
   int rc = ls_check_launch("ls_attn_plan_kernel");
@@ -879,4 +881,75 @@ extern "C" int ls_nosa_attn_varlen(const void* q, int64_t q_row_stride, const vo
                   batch, total_q, total_k, max_seqlen_k, num_heads, num_kv_heads, head_dim,
                   dtype, topk_idx, take, block_size, softmax_scale, 1, out, lse, workspace,
                   workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of ls_sparse_attn_varlen: the workspace is a static
+// device array of the library instead of a caller buffer.  In host code
+// `scratch` only names the symbol; its device address (one per GPU) comes
+// from hipGetSymbolAddress, taken once per device with that device current.
+// ---------------------------------------------------------------------------
+#define LS_MAX_DEVICES 64  // LS_NOALLOC_SCRATCH_BYTES comes from the public header
+
+static __device__ __align__(256) uint8_t scratch[LS_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[LS_MAX_DEVICES] = {};
+
+// Device address of `scratch` on the device that owns `stream`.
+int scratch_for_stream(hipStream_t stream, void** ptr) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return ls_fail(LS_ERR_HIP, "ls_sparse_attn_varlen_noalloc: no device for the stream: %s",
+                   hipGetErrorString(e));
+  LS_REQUIRE(dev >= 0 && dev < LS_MAX_DEVICES, LS_ERR_UNSUPPORTED,
+             "ls_sparse_attn_varlen_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if ((e = hipGetDevice(&cur)) != hipSuccess)
+      return ls_fail(LS_ERR_HIP, "ls_sparse_attn_varlen_noalloc: %s", hipGetErrorString(e));
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return ls_fail(LS_ERR_HIP, "ls_sparse_attn_varlen_noalloc: %s", hipGetErrorString(e));
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p)
+      return ls_fail(LS_ERR_HIP, "ls_sparse_attn_varlen_noalloc: scratch address on device %d: %s",
+                     dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return LS_OK;
+}
+}  // namespace
+
+extern "C" int ls_sparse_attn_varlen_noalloc(
+    const void* q, int64_t q_row_stride, const void* k, int64_t k_row_stride, const void* v,
+    int64_t v_row_stride, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t batch,
+    int64_t total_q, int64_t total_k, int32_t max_seqlen_q, int32_t max_seqlen_k,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+    const int32_t* topk_idx, int32_t take, int32_t block_size, float softmax_scale,
+    int32_t causal, void* out, float* lse, int32_t* status, void* stream) {
+  (void)max_seqlen_q;
+  // The size check comes first and touches no device.
+  LS_REQUIRE(batch >= 0 && total_k >= 0 && num_kv_heads > 0, LS_ERR_INVALID,
+             "ls_sparse_attn_varlen_noalloc: bad sizes");
+  const size_t need = attn_ws(total_k, batch, num_kv_heads, false).total;
+  LS_REQUIRE(need <= LS_NOALLOC_SCRATCH_BYTES, LS_ERR_UNSUPPORTED,
+             "ls_sparse_attn_varlen_noalloc: %lld keys in %d sequences of %d KV heads need "
+             "%zu bytes of scratch, above the static %u (use ls_sparse_attn_varlen with a "
+             "workspace)",
+             (long long)total_k, batch, num_kv_heads, need, LS_NOALLOC_SCRATCH_BYTES);
+  if (total_q == 0 || batch == 0) return LS_OK;
+  void* ws = nullptr;
+  const int rc = scratch_for_stream((hipStream_t)stream, &ws);
+  if (rc) return rc;
+  return attn_run("ls_sparse_attn_varlen_noalloc", q, q_row_stride, k, k_row_stride, v,
+                  v_row_stride, nullptr, 0, 0, cu_seqlens_q, cu_seqlens_k, batch, total_q,
+                  total_k, max_seqlen_k, num_heads, num_kv_heads, head_dim, dtype, topk_idx,
+                  take, block_size, softmax_scale, causal, out, lse, ws,
+                  LS_NOALLOC_SCRATCH_BYTES, stream, status);
 }
