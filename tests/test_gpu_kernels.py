@@ -52,6 +52,24 @@ def _selector(H=32, G=2, D=128, R=4, RD=32, seed=0):
     return s.requires_grad_(False).to(DEV)
 
 
+@pytest.mark.parametrize("geom", [(32, 16, 128), (32, 16, 64), (48, 16, 128), (32, 8, 128)])
+def test_compress_k_geometries(geom):
+    """Half-window sharing (windows of two strides, 16 or 32 windows per block) and
+    the direct path for other geometries, across sequence and block boundaries."""
+    ks, st, D = geom
+    lens = [100, 31, ks, ks + st, 0, 77, 700, 16 * st + ks]
+    cu = _cu(lens)
+    torch.manual_seed(2)
+    k = torch.randn(cu[-1], 2, D).to(torch.bfloat16)
+    got, cu_c = compress_k(k.to(DEV), torch.tensor(cu, dtype=torch.int32, device=DEV),
+                           kernel_size=ks, kernel_stride=st)
+    want, cu_want = oracle.compress_k(k, cu, kernel_size=ks, kernel_stride=st)
+    assert cu_c.cpu().tolist() == cu_want.tolist()
+    got = got.cpu()
+    assert (got != want).float().mean().item() < 1e-3
+    assert _ulp_diff(got, want).max().item() <= 1.0
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_compress_k_matches_oracle(dtype):
     lens = [100, 31, 32, 48, 0, 77, 5000]
