@@ -691,6 +691,111 @@ __device__ __forceinline__ void ls_topk_row(const void* __restrict__ P, int64_t 
   }
 }
 
+// The same for 16-bit scores of rows of more than four slots, emitting from
+// the gathered candidates: the keys >= lo (lo = the kk-th largest of the
+// lanes' two largest keys, a lower bound of the kk-th key) are packed as
+// key << 16 | column into at most four slots in column order, the kk-th key T
+// is bisected on them from the common bit prefix of lo and the row maximum,
+// and the chosen columns (keys > T, then the lowest-column ties) are written
+// from those four slots instead of from all NS.  When the packed set would
+// overflow its 256 entries the row takes ls_topk_row.
+template <int NS>
+__device__ __forceinline__ void ls_topk_row16(const void* __restrict__ P, int64_t base, int cn,
+                                              int kk, int lo_end, int lane,
+                                              int32_t* __restrict__ orow,
+                                              uint32_t* __restrict__ scr) {
+  if (NS <= 4 || kk < 1 || kk > 128)
+    return ls_topk_row<NS, false>(P, base, cn, kk, lo_end, lane, orow, scr);
+  uint32_t key[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) key[s] = ((const uint16_t*)P)[base + min(s * 64 + lane, cn - 1)];
+  uint32_t m1 = 0u, m2 = 0u;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    key[s] = s * 64 + lane < cn ? ls_order_key16((uint16_t)key[s]) : 0u;
+    m2 = max(m2, min(m1, key[s]));
+    m1 = max(m1, key[s]);
+  }
+  const uint32_t mm[2] = {m1, m2};
+  const uint32_t lo = ls_kth_bisect<2>(mm, kk, 0u, 15);
+  int n = 0;
+  if (lo != 0u) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const bool sv = key[s] >= lo;
+      const uint64_t mk = __ballot(sv);
+      const int pos = n + ls_lanes_below(mk);
+      if (sv && pos < 256) scr[pos] = (key[s] << 16) | (uint32_t)(s * 64 + lane);
+      n += __popcll(mk);
+    }
+  }
+  if (lo == 0u || n > 256) {  // no usable bound: every slot is searched and emitted
+    const uint32_t T = ls_kth_bisect<NS>(key, kk, 0u, 15);
+    int gt = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) gt += __popcll(__ballot(key[s] > T));
+    const int m = kk - gt;
+    int out_pos = lo_end, eq_before = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int c = s * 64 + lane;
+      const bool valid = c < cn;
+      const bool eq = valid && key[s] == T;
+      const uint64_t eq_mask = __ballot(eq);
+      const int eq_rank = eq_before + ls_lanes_below(eq_mask);
+      const bool sel = valid && (key[s] > T || (eq && eq_rank < m));
+      const uint64_t sel_mask = __ballot(sel);
+      const int pos = out_pos + ls_lanes_below(sel_mask);
+      if (sel && pos < lo_end + kk) orow[pos] = lo_end + c;
+      out_pos += __popcll(sel_mask);
+      eq_before += __popcll(eq_mask);
+    }
+    return;
+  }
+  uint32_t pk[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pk[i] = i * 64 + lane < n ? scr[i * 64 + lane] : 0u;
+  uint32_t hi = m1;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, LS_WAVE));
+  hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)hi);
+  // T: the largest 16-bit key with #{key >= T} >= kk, sharing lo's and hi's
+  // common bit prefix.
+  uint32_t T = lo;
+  const uint32_t d = lo ^ hi;
+  if (d != 0u) {
+    const int tb = 31 - __builtin_clz(d);
+    T = lo & ~((2u << tb) - 1u);
+#pragma unroll 1
+    for (int bit = tb; bit >= 0; --bit) {
+      const uint32_t cand = (T | (1u << bit)) << 16;
+      int cnt = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cnt += __popcll(__ballot(pk[i] >= cand));
+      if (cnt >= kk) T |= 1u << bit;
+    }
+  }
+  const uint32_t above = (T << 16) | 0xffffu;  // packed keys above T
+  int gt = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) gt += __popcll(__ballot(pk[i] > above));
+  const int m = kk - gt;
+  int out_pos = lo_end, eq_before = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool valid = i * 64 + lane < n;
+    const bool eq = valid && (pk[i] >> 16) == T;
+    const uint64_t eq_mask = __ballot(eq);
+    const int eq_rank = eq_before + ls_lanes_below(eq_mask);
+    const bool sel = valid && (pk[i] > above || (eq && eq_rank < m));
+    const uint64_t sel_mask = __ballot(sel);
+    const int pos = out_pos + ls_lanes_below(sel_mask);
+    if (sel && pos < lo_end + kk) orow[pos] = lo_end + (int)(pk[i] & 0xffffu);
+    out_pos += __popcll(sel_mask);
+    eq_before += __popcll(eq_mask);
+  }
+}
+
 template <int KPL, bool KEY32>
 __global__ __launch_bounds__(256) void ls_topk_kernel(
     const void* __restrict__ P, int64_t p_stride, const int32_t* __restrict__ cu_q,
@@ -740,11 +845,19 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
   if (n_slots <= 1) return ls_topk_row<1, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
   if (n_slots <= 2) return ls_topk_row<2, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
   if (n_slots <= 4 || KPL <= 4) return ls_topk_row<(KPL < 4 ? KPL : 4), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
-  if (n_slots <= 8 || KPL <= 8) return ls_topk_row<(KPL < 8 ? KPL : 8), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
-  if (n_slots <= 16 || KPL <= 16) return ls_topk_row<(KPL < 16 ? KPL : 16), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
-  if (n_slots <= 32 || KPL <= 32) return ls_topk_row<(KPL < 32 ? KPL : 32), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
-  if (n_slots <= 64 || KPL <= 64) return ls_topk_row<(KPL < 64 ? KPL : 64), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
-  return ls_topk_row<KPL, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+  if constexpr (!KEY32) {
+    if (n_slots <= 8 || KPL <= 8) return ls_topk_row16<(KPL < 8 ? KPL : 8)>(P, base, cn, kk, lo_end, lane, orow, scr);
+    if (n_slots <= 16 || KPL <= 16) return ls_topk_row16<(KPL < 16 ? KPL : 16)>(P, base, cn, kk, lo_end, lane, orow, scr);
+    if (n_slots <= 32 || KPL <= 32) return ls_topk_row16<(KPL < 32 ? KPL : 32)>(P, base, cn, kk, lo_end, lane, orow, scr);
+    if (n_slots <= 64 || KPL <= 64) return ls_topk_row16<(KPL < 64 ? KPL : 64)>(P, base, cn, kk, lo_end, lane, orow, scr);
+    return ls_topk_row16<KPL>(P, base, cn, kk, lo_end, lane, orow, scr);
+  } else {
+    if (n_slots <= 8 || KPL <= 8) return ls_topk_row<(KPL < 8 ? KPL : 8), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+    if (n_slots <= 16 || KPL <= 16) return ls_topk_row<(KPL < 16 ? KPL : 16), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+    if (n_slots <= 32 || KPL <= 32) return ls_topk_row<(KPL < 32 ? KPL : 32), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+    if (n_slots <= 64 || KPL <= 64) return ls_topk_row<(KPL < 64 ? KPL : 64), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+    return ls_topk_row<KPL, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+  }
 }
 
 // ---------------------------------------------------------------------------
