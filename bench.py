@@ -269,9 +269,11 @@ def model_bench(args, dev) -> None:
     stages = {
         "rmsnorm": lambda: minicpm.rms_layernorm(x, L.input_norm, cfg.rms_norm_eps, out=h),
         "qkv_gemm": lambda: F.linear(h, L.w_qkv),
-        "rope": lambda: minicpm.rope_inplace(qkv, pos, cos, sin, n_q_heads=H, n_k_heads=G,
-                                             k_col_offset=H * D, check_positions=False),
-        "compress_k": lambda: compress_k(k, cu, cu_seqlens_host=cu_host),
+        "rope_q": lambda: minicpm.rope_inplace(qkv, pos, cos, sin, n_q_heads=H, n_k_heads=0,
+                                               k_col_offset=H * D, check_positions=False),
+        "rope_k_compress": lambda: minicpm.rope_k_compress(
+            qkv, pos, cos, sin, cu, cu_host, n_k_heads=G, k_col_offset=H * D,
+            check_positions=False),
         "select": lambda: leanselect_prefill_topk_idx(q, kc, cu, cu_c, L.selector, **kw),
         "sparse_attention": lambda: sparse_attention(q, k, v, cu, cu, N, N, sel_ids),
         "o_gemm": lambda: F.linear(attn.view(N, H * D), L.w_o),

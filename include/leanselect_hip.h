@@ -385,6 +385,28 @@ int ls_rope_inplace(void* x, int64_t row_stride, const int32_t* positions, int64
                     int32_t dtype, void* stream);
 
 /*
+ * Rotary embedding of the key heads fused with the compressed keys: rotates
+ * the n_k_heads key heads (columns k_col_offset + [0, n_k_heads * 128)) of every
+ * row in place exactly as ls_rope_inplace, and writes the compressed keys of
+ * the rotated rows as ls_compress_k_varlen would (windows of 32 rows at
+ * stride 16 inside each sequence of cu_seqlens, float32 sums, one rounding):
+ *   kc_out [total_atoms, n_k_heads, 128] contiguous, cu_out int32 [batch + 1].
+ * Each rotated row is summed while it is written, so the keys are not read
+ * again.  head_dim 128, kernel 32 / stride 16; workspace from
+ * ls_rope_k_compress_workspace_size.
+ * Replaces apply_rotary_pos_emb on the keys (leanselect/models/minicpm.py:1027-1070,
+ * 2218-2222) followed by CompressK.forward (minicpm.py:1158-1185) on them.
+ */
+size_t ls_rope_k_compress_workspace_size(int64_t n_rows, int32_t batch, int32_t n_k_heads,
+                                         int32_t head_dim);
+int ls_rope_k_compress(void* x, int64_t row_stride, const int32_t* positions,
+                       const int32_t* cu_seqlens, int32_t batch, int64_t n_rows,
+                       int32_t n_k_heads, int64_t k_col_offset, int32_t head_dim,
+                       const float* cos_table, const float* sin_table, int64_t table_rows,
+                       int32_t dtype, void* kc_out, int64_t total_atoms, int32_t* cu_out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * SiLU-gated activation: out = round(round(silu(g)) * u), g = columns
  * [0, inter) and u = columns [inter, 2 inter) of gate_up.
  * Replaces act_fn(gate_proj(x)) * up_proj(x) in MiniCPMMLP.forward

@@ -69,6 +69,10 @@ SIGNATURES = {
         _i32, [_p, _i64, _p, _i64, _f32, _p, _i64, _i32, _f32, _i32, _p, _i64, _p]),
     "ls_rope_inplace": (
         _i32, [_p, _i64, _p, _i64, _i32, _i32, _i64, _i32, _p, _p, _i64, _i32, _p]),
+    "ls_rope_k_compress_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
+    "ls_rope_k_compress": (
+        _i32, [_p, _i64, _p, _p, _i32, _i64, _i32, _i64, _i32, _p, _p, _i64, _i32, _p, _i64, _p,
+               _p, _sz, _p]),
     "ls_silu_mul": (_i32, [_p, _i64, _i64, _i32, _i32, _p, _i64, _p]),
     "ls_embed_scale": (_i32, [_p, _i64, _p, _i64, _i32, _f32, _i32, _p, _p]),
 }

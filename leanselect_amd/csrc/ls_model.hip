@@ -151,6 +151,85 @@ __global__ __launch_bounds__(256) void ls_rope_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Rotary embedding of the key heads fused with the compressed keys
+// (producer-side compression: the mean of 32 post-RoPE key rows at stride 16,
+// CompressK.forward, minicpm.py:1158-1185, formed while the rows are rotated
+// instead of re-reading them).  Window a of a sequence is the sum of its half
+// windows a and a + 1 (16 rows each), so:
+//   ls_rope_k_half_kernel  one workgroup per 16-row half window of one
+//     sequence, one thread per (key head, rotation pair d / d + 64): rotates
+//     the rows in place exactly as ls_rope_kernel and sums the rounded results
+//     in float32 in row order into hsum[half][head][128];
+//   ls_k_atoms_kernel      kc[atom][head][d] = round((hsum[a][head][d] +
+//     hsum[a + 1][head][d]) / 32): the same sums, in the same order, as
+//     ls_compress_half_kernel forms from the rotated rows.
+// hw_off[b] = sum_{b' < b} ceil(len(b') / 16) (first half window of each
+// sequence); cu_out[b] as ls_compress_k_varlen.
+// ---------------------------------------------------------------------------
+__global__ void ls_rope_k_plan_kernel(const int32_t* __restrict__ cu, int batch,
+                                      int32_t* __restrict__ hw_off, int32_t* __restrict__ cu_out) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int32_t h = 0, a = 0;
+  hw_off[0] = 0;
+  cu_out[0] = 0;
+  for (int b = 0; b < batch; ++b) {
+    const int len = cu[b + 1] - cu[b];
+    h += len > 0 ? (len + 15) / 16 : 0;
+    a += len >= 32 ? (len - 32) / 16 + 1 : 0;
+    hw_off[b + 1] = h;
+    cu_out[b + 1] = a;
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(1024) void ls_rope_k_half_kernel(
+    uint16_t* __restrict__ x, int64_t xs, const int32_t* __restrict__ pos,
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ hw_off, int batch, int n_k,
+    int64_t k_off, const float* __restrict__ cosb, const float* __restrict__ sinb,
+    int64_t table_rows, float* __restrict__ hsum) {
+  const int64_t hw = blockIdx.x;
+  if (hw >= hw_off[batch]) return;
+  const int b = ls_find_segment(hw_off, batch, hw);
+  const int64_t r0 = (int64_t)cu[b] + 16 * (hw - hw_off[b]);
+  const int rows = (int)min((int64_t)16, (int64_t)cu[b + 1] - r0);
+  const int hd = threadIdx.x >> 6, d = threadIdx.x & 63;
+  float s1 = 0.f, s2 = 0.f;
+  for (int r = 0; r < rows; ++r) {
+    const int64_t row = r0 + r;
+    int64_t p = pos[row];
+    p = p < 0 ? 0 : (p >= table_rows ? table_rows - 1 : p);
+    uint16_t* xr = x + row * xs + k_off + (int64_t)hd * 128;
+    const float x1 = LsElem<DT>::to_f(xr[d]), x2 = LsElem<DT>::to_f(xr[d + 64]);
+    const float y1 = __fadd_rn(__fmul_rn(x1, cosb[p * 128 + d]), __fmul_rn(-x2, sinb[p * 128 + d]));
+    const float y2 = __fadd_rn(__fmul_rn(x2, cosb[p * 128 + 64 + d]), __fmul_rn(x1, sinb[p * 128 + 64 + d]));
+    const uint16_t o1 = LsElem<DT>::from_f(y1), o2 = LsElem<DT>::from_f(y2);
+    xr[d] = o1;
+    xr[d + 64] = o2;
+    s1 += LsElem<DT>::to_f(o1);
+    s2 += LsElem<DT>::to_f(o2);
+  }
+  float* hs = hsum + (hw * n_k + hd) * 128;
+  hs[d] = s1;
+  hs[d + 64] = s2;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void ls_k_atoms_kernel(
+    const float* __restrict__ hsum, const int32_t* __restrict__ hw_off,
+    const int32_t* __restrict__ cu_out, int batch, int n_k, int64_t total_atoms,
+    uint16_t* __restrict__ kc) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per_atom = (int64_t)n_k * 128;
+  const int64_t atom = i / per_atom;
+  if (atom >= total_atoms || atom >= cu_out[batch]) return;
+  const int e = (int)(i - atom * per_atom);
+  const int b = ls_find_segment(cu_out, batch, atom);
+  const int64_t h = hw_off[b] + (atom - cu_out[b]);
+  const float v = (hsum[h * per_atom + e] + hsum[(h + 1) * per_atom + e]) / 32.f;
+  kc[atom * per_atom + e] = LsElem<DT>::from_f(v);
+}
+
+// ---------------------------------------------------------------------------
 // SiLU-gated activation (MiniCPMMLP.forward, minicpm.py:1098-1130:
 // act_fn(gate_proj(x)) * up_proj(x)) on one [n, 2 I] GEMM output holding gate
 // columns [0, I) and up columns [I, 2 I):
@@ -345,4 +424,63 @@ extern "C" int ls_embed_scale(const int32_t* ids, int64_t n, const void* table, 
     hipLaunchKernelGGL(ls_embed_kernel<LS_F16>, grid, dim3(256), 0, s, ids, n,
                        (const uint16_t*)table, vocab, hidden, scale, (uint16_t*)out);
   return ls_check_launch("ls_embed_kernel");
+}
+
+extern "C" size_t ls_rope_k_compress_workspace_size(int64_t n_rows, int32_t batch,
+                                                    int32_t n_k_heads, int32_t head_dim) {
+  (void)head_dim;
+  const int64_t halves = (n_rows > 0 ? n_rows : 0) / 16 + (batch > 0 ? batch : 0);
+  return ls_align256((size_t)(batch + 1) * 4) +
+         ls_align256((size_t)halves * (n_k_heads > 0 ? n_k_heads : 0) * 128 * 4);
+}
+
+extern "C" int ls_rope_k_compress(void* x, int64_t row_stride, const int32_t* positions,
+                                  const int32_t* cu_seqlens, int32_t batch, int64_t n_rows,
+                                  int32_t n_k_heads, int64_t k_col_offset, int32_t head_dim,
+                                  const float* cos_table, const float* sin_table,
+                                  int64_t table_rows, int32_t dtype, void* kc_out,
+                                  int64_t total_atoms, int32_t* cu_out, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  if (int rc = ls_model_dtype(dtype, "ls_rope_k_compress")) return rc;
+  LS_REQUIRE(head_dim == 128, LS_ERR_UNSUPPORTED,
+             "ls_rope_k_compress: head_dim must be 128 (got %d)", head_dim);
+  LS_REQUIRE(n_rows >= 0 && batch >= 0 && n_k_heads > 0 && n_k_heads <= 16 && table_rows > 0 &&
+                 total_atoms >= 0,
+             LS_ERR_INVALID, "ls_rope_k_compress: bad sizes");
+  LS_REQUIRE(k_col_offset >= 0 && row_stride >= k_col_offset + (int64_t)n_k_heads * head_dim,
+             LS_ERR_INVALID, "ls_rope_k_compress: key heads must lie inside the row");
+  LS_REQUIRE(cu_seqlens && cu_out, LS_ERR_INVALID, "ls_rope_k_compress: null cu_seqlens");
+  const size_t need = ls_rope_k_compress_workspace_size(n_rows, batch, n_k_heads, head_dim);
+  LS_REQUIRE(workspace && workspace_bytes >= need, LS_ERR_WORKSPACE,
+             "ls_rope_k_compress: workspace needs %zu bytes", need);
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* hw_off = (int32_t*)workspace;
+  float* hsum = (float*)((char*)workspace + ls_align256((size_t)(batch + 1) * 4));
+  hipLaunchKernelGGL(ls_rope_k_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens, batch, hw_off,
+                     cu_out);
+  if (int rc = ls_check_launch("ls_rope_k_plan_kernel")) return rc;
+  if (n_rows == 0 || batch == 0) return LS_OK;
+  LS_REQUIRE(x && positions && cos_table && sin_table && (total_atoms == 0 || kc_out),
+             LS_ERR_INVALID, "ls_rope_k_compress: null tensor");
+  const int64_t halves = n_rows / 16 + batch;
+  const dim3 hgrid((unsigned)halves), hblock((unsigned)(64 * n_k_heads));
+  const dim3 agrid((unsigned)((total_atoms * n_k_heads * 128 + 255) / 256));
+  if (dtype == LS_BF16) {
+    hipLaunchKernelGGL(ls_rope_k_half_kernel<LS_BF16>, hgrid, hblock, 0, s, (uint16_t*)x,
+                       row_stride, positions, cu_seqlens, hw_off, batch, n_k_heads, k_col_offset,
+                       cos_table, sin_table, table_rows, hsum);
+    if (int rc = ls_check_launch("ls_rope_k_half_kernel")) return rc;
+    if (total_atoms > 0)
+      hipLaunchKernelGGL(ls_k_atoms_kernel<LS_BF16>, agrid, dim3(256), 0, s, hsum, hw_off, cu_out,
+                         batch, n_k_heads, total_atoms, (uint16_t*)kc_out);
+  } else {
+    hipLaunchKernelGGL(ls_rope_k_half_kernel<LS_F16>, hgrid, hblock, 0, s, (uint16_t*)x,
+                       row_stride, positions, cu_seqlens, hw_off, batch, n_k_heads, k_col_offset,
+                       cos_table, sin_table, table_rows, hsum);
+    if (int rc = ls_check_launch("ls_rope_k_half_kernel")) return rc;
+    if (total_atoms > 0)
+      hipLaunchKernelGGL(ls_k_atoms_kernel<LS_F16>, agrid, dim3(256), 0, s, hsum, hw_off, cu_out,
+                         batch, n_k_heads, total_atoms, (uint16_t*)kc_out);
+  }
+  return ls_check_launch("ls_k_atoms_kernel");
 }

@@ -40,6 +40,7 @@ __all__ = [
     "rms_layernorm",
     "add_rms_layernorm",
     "rope_inplace",
+    "rope_k_compress",
     "silu_mul",
     "embed_scale",
 ]
@@ -174,6 +175,46 @@ def rope_inplace(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, si
     return x
 
 
+def rope_k_compress(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
+                    sin: torch.Tensor, cu_seqlens: torch.Tensor, cu_host: list[int], *,
+                    n_k_heads: int, k_col_offset: int, head_dim: int = 128,
+                    check_positions: bool = True):
+    """Rotate the key heads of ``x [n, width]`` in place (as :func:`rope_inplace`)
+    and return their compressed keys ``(kc [A, n_k_heads, D], cu_seqlens_compressed)``
+    -- ``CompressK.forward`` (minicpm.py:1158-1185) of the rotated keys, formed
+    while they are written (windows of 32 at stride 16)."""
+    _rows(x, "x")
+    dev = _hip.require_gpu(x, positions, cos, sin, cu_seqlens)
+    if positions.dtype != torch.int32 or positions.shape != (x.shape[0],):
+        raise ValueError("positions must be int32 [n]")
+    if cu_seqlens.dtype != torch.int32 or cu_seqlens.numel() != len(cu_host):
+        raise ValueError("cu_seqlens must be int32 [batch + 1] matching cu_host")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape \
+            or cos.ndim != 2 or cos.shape[1] != head_dim:
+        raise ValueError("cos/sin must be float32 [table_rows, head_dim]")
+    if x.shape[1] < k_col_offset + n_k_heads * head_dim:
+        raise ValueError("the key heads must lie inside x's columns")
+    if check_positions and positions.numel():
+        lo, hi = int(positions.min()), int(positions.max())
+        if lo < 0 or hi >= cos.shape[0]:
+            raise ValueError(f"positions must lie in [0, {cos.shape[0]}) (got {lo}..{hi})")
+    batch = len(cu_host) - 1
+    lens = [cu_host[i + 1] - cu_host[i] for i in range(batch)]
+    total_atoms = sum((n - 32) // 16 + 1 for n in lens if n >= 32)
+    kc = torch.empty((total_atoms, n_k_heads, head_dim), dtype=x.dtype, device=dev)
+    cu_c = torch.empty((batch + 1,), dtype=torch.int32, device=dev)
+    L = _hip.lib()
+    ws = _hip.workspace(L.ls_rope_k_compress_workspace_size(x.shape[0], batch, n_k_heads,
+                                                            head_dim), dev)
+    _hip.check(L.ls_rope_k_compress(
+        x.data_ptr(), x.stride(0), positions.contiguous().data_ptr(), cu_seqlens.data_ptr(), batch,
+        x.shape[0], n_k_heads, k_col_offset, head_dim, cos.contiguous().data_ptr(),
+        sin.contiguous().data_ptr(), cos.shape[0], _hip.dtype_code(x.dtype),
+        kc.data_ptr() if total_atoms else None, total_atoms, cu_c.data_ptr(), ws.data_ptr(),
+        ws.numel(), _hip.stream_of(dev)), "ls_rope_k_compress")
+    return kc, cu_c
+
+
 def silu_mul(gate_up: torch.Tensor, inter: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """``silu(gate) * up`` for ``gate_up [n, 2*inter]`` = [gate | up] (minicpm.py:1098-1135)."""
     _rows(gate_up, "gate_up")
@@ -287,15 +328,24 @@ class MiniCPMLeanSelect:
         N = h.shape[0]
         qkv = F.linear(h, L.w_qkv)
         cos, sin = self.rope_tables(max(cu_host[i + 1] - cu_host[i] for i in range(len(cu_host) - 1)))
-        rope_inplace(qkv, positions, cos, sin, n_q_heads=H, n_k_heads=G, k_col_offset=H * D,
-                     head_dim=D, check_positions=False)
+        # Queries rotate in place; the keys rotate in the pass that also forms
+        # their compressed keys (the attention layer then does not re-read them).
+        fused = cfg.kernel_size == 32 and cfg.kernel_stride == 16
+        rope_inplace(qkv, positions, cos, sin, n_q_heads=H, n_k_heads=0 if fused else G,
+                     k_col_offset=H * D, head_dim=D, check_positions=False)
+        compressed = None
+        if fused:
+            compressed = rope_k_compress(qkv, positions, cos, sin, cu_seqlens, cu_host,
+                                         n_k_heads=G, k_col_offset=H * D, head_dim=D,
+                                         check_positions=False)
         q = qkv[:, : H * D].view(N, H, D)
         k = qkv[:, H * D: H * D + G * D].view(N, G, D)
         v = qkv[:, H * D + G * D:].view(N, G, D)
         attn, ids = leanselect_sparse_prefill(
             q, k, v, cu_seqlens, L.selector, topk=cfg.topk, local_blocks=cfg.local_blocks,
             init_blocks=cfg.init_blocks, block_size=cfg.block_size, kernel_size=cfg.kernel_size,
-            kernel_stride=cfg.kernel_stride, cu_seqlens_host=cu_host, return_topk_idx=True)
+            kernel_stride=cfg.kernel_stride, cu_seqlens_host=cu_host, return_topk_idx=True,
+            compressed=compressed)
         o = F.linear(attn.view(N, H * D), L.w_o)
         if return_parts:
             return o, dict(qkv=qkv, attn=attn, topk_idx=ids)

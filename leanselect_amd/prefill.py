@@ -39,17 +39,23 @@ def leanselect_sparse_prefill(
     kernel_stride: int = 16,
     cu_seqlens_host: list[int] | None = None,
     return_topk_idx: bool = False,
+    compressed: tuple[torch.Tensor, torch.Tensor] | None = None,
 ):
     """``(out [total, H, D], topk_idx [G, total, take])`` for packed prefill sequences.
 
     ``topk`` is the total page budget (forced pages included), i.e. the
     reference's ``self.topk = topk + window_size // block_size``.
+    ``compressed`` = ``(kc, cu_seqlens_compressed)`` when the producer of ``k``
+    already formed the compressed keys (``minicpm.rope_k_compress``).
     """
     host = cu_seqlens_host if cu_seqlens_host is not None else cu_seqlens.tolist()
     max_len = max(host[i + 1] - host[i] for i in range(len(host) - 1))
     range_push("compress")
-    kc, cu_c = compress_k(k, cu_seqlens, kernel_size=kernel_size, kernel_stride=kernel_stride,
-                          cu_seqlens_host=host)
+    if compressed is not None:
+        kc, cu_c = compressed
+    else:
+        kc, cu_c = compress_k(k, cu_seqlens, kernel_size=kernel_size,
+                              kernel_stride=kernel_stride, cu_seqlens_host=host)
     range_pop()
     range_push("stage 1")
     ids = leanselect_prefill_topk_idx(

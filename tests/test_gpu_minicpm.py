@@ -218,3 +218,33 @@ def test_prefill_ragged_with_short_sequences_and_wide_local_window():
         alone = model.prefill(s)[0]
         cs = torch.nn.functional.cosine_similarity(packed[i].double(), alone.double(), dim=0)
         assert float(cs) > 0.999, (i, float(cs))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_k_compress_equals_rope_then_compress(dtype):
+    """The fused pass (keys rotated while their compressed keys are formed) gives
+    bit for bit the rotated keys of ls_rope_inplace and the compressed keys of
+    ls_compress_k_varlen on them, on a ragged batch with sequences shorter than
+    a window and lengths off the 16-row grid."""
+    from leanselect_amd.ops import compress_k
+    lens = [100, 31, 32, 47, 0, 1000, 16, 7]
+    cu_host = [0]
+    for n in lens:
+        cu_host.append(cu_host[-1] + n)
+    N, H, G, D = cu_host[-1], 4, 2, 128
+    g = torch.Generator(device="cpu").manual_seed(9)
+    x = (torch.randn(N, H * D + 2 * G * D, generator=g) * 2).to(dtype).to(DEV)
+    pos = torch.cat([torch.arange(n, dtype=torch.int32) for n in lens]).to(DEV)
+    cos, sin = minicpm.rotary_tables(D, 1024, 10000.0, DEV)
+    cu = torch.tensor(cu_host, dtype=torch.int32, device=DEV)
+    ref = x.clone()
+    minicpm.rope_inplace(ref, pos, cos, sin, n_q_heads=0, n_k_heads=G, k_col_offset=H * D)
+    want_kc, want_cu = compress_k(ref[:, H * D : H * D + G * D].view(N, G, D), cu,
+                                  cu_seqlens_host=cu_host)
+    got = x.clone()
+    kc, cu_c = minicpm.rope_k_compress(got, pos, cos, sin, cu, cu_host, n_k_heads=G,
+                                       k_col_offset=H * D)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)  # keys rotated in place, every other column untouched
+    assert torch.equal(cu_c, want_cu)
+    assert torch.equal(kc, want_kc)
