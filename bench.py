@@ -215,6 +215,57 @@ def cpu_baseline(case, attn_rows: int, threads: int, runs: int = 3) -> dict:
     }
 
 
+def cpu_baseline_nosa(case, cis, n_rows: int, threads: int, runs: int = 3) -> dict:
+    """The NOSA path restated on the host CPU (the oracle, float64), ms per layer.
+
+    Compressed keys run in full; the atom scores, the two-stage page selection
+    and the CIS-weighted attention run on an even sample of query rows and are
+    scaled to the layer.  Each part is the median of ``runs`` warm runs.
+    """
+    import oracle
+
+    torch.set_num_threads(threads)
+    q, k, v, c = case.q.cpu(), case.k.cpu(), case.v.cpu(), cis.cpu()
+    cu = case.cu_host
+    N = cu[-1]
+    max_len = max(cu[b + 1] - cu[b] for b in range(len(cu) - 1))
+    sel = case.selector
+    qf, kf = oracle.fused_weights(*[getattr(sel, n).detach().float().cpu()
+                                    for n in ("head_mix", "kv_head_mix", "q_proj", "k_proj")],
+                                  dtype=q.dtype)
+    kc, cu_c = oracle.reference_compress_k(k, cu)
+    step = max(1, N // n_rows)
+    rows = list(range(step // 2, N, step))
+    kw = dict(topk=case.topk, init_blocks=case.init_blocks, local_blocks=case.local_blocks,
+              select_blocks=24, rows=rows)
+
+    def select():
+        atoms = oracle.nosa_atom_scores(q, kc, cu, cu_c, qf, kf, rows=rows)
+        return oracle.nosa_select_prefill(atoms, c, cu, cu_c, cu, max_len, max_len, **kw)
+
+    ids = select()
+    t_c, n_c = _median_s(lambda: oracle.reference_compress_k(k, cu), runs, 60.0)
+    t_s, n_s = _median_s(select, runs, 60.0)
+    t_a, n_a = _median_s(lambda: oracle.nosa_attention(q, k, v, c, cu, cu, ids, rows=rows,
+                                                       ids_rows_aligned=True), runs, 60.0)
+    scale = N / len(rows)
+    ms = 1e3 * (t_c + (t_s + t_a) * scale)
+    return {
+        "value": round(ms, 1),
+        "unit": "ms/layer",
+        "cores": threads,
+        "kind": "port",
+        "cpu_model": _cpu_model(),
+        "stages_ms": {"compress_k": round(1e3 * t_c, 1), "select": round(1e3 * t_s * scale, 1),
+                      "sparse_attention": round(1e3 * t_a * scale, 1)},
+        "sample": (f"the NOSA path restated in float64 on the host CPU ({threads} threads), "
+                   f"median of {min(n_c, n_s, n_a)}-{max(n_c, n_s, n_a)} warm runs: compressed "
+                   f"keys of all {N} tokens, then atom scores, two-stage page selection and "
+                   f"CIS-weighted attention on {len(rows)} evenly spaced query rows "
+                   f"({1e3 * (t_s + t_a):.0f} ms) scaled by {scale:.1f}"),
+    }
+
+
 def model_bench(args, dev) -> None:
     """Whole-model prefill: seconds per prefill plus one layer's stage breakdown."""
     import torch.nn.functional as F
@@ -329,6 +380,8 @@ def main() -> None:
     ap.add_argument("--kernel-iters", type=int, default=5)
     ap.add_argument("--cpu-attn-rows", type=int, default=1024,
                     help="query rows of the CPU baseline's attention sample")
+    ap.add_argument("--cpu-nosa-rows", type=int, default=256,
+                    help="query rows of the NOSA CPU baseline's selection and attention sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the secondary attention timing on plans without planted topics")
@@ -477,7 +530,7 @@ def main() -> None:
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
-            "traffic": None if nosa else _traffic(args.workload),
+            "traffic": _traffic(args.workload + (":nosa" if nosa else "")),
             "algorithmic_flops": attn_flops,
             "avg_keys_per_row": round(n_keys / (G * N), 1),
         },
@@ -487,13 +540,16 @@ def main() -> None:
             "attention_without_topics": secondary_plans,
         },
     }
-    if not args.no_cpu_baseline and not nosa:
+    if not args.no_cpu_baseline:
         # The host cores of this GPU's share (OMP_NUM_THREADS on a shared box).
         threads = len(os.sched_getaffinity(0))
         if os.environ.get("OMP_NUM_THREADS", "").isdigit():
             threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
         print(f"[bench] CPU baseline on {threads} threads ...", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(case, args.cpu_attn_rows, threads)
+        if nosa:
+            result["cpu_baseline"] = cpu_baseline_nosa(case, cis, args.cpu_nosa_rows, threads)
+        else:
+            result["cpu_baseline"] = cpu_baseline(case, args.cpu_attn_rows, threads)
     print(json.dumps(result), flush=True)
 
 
