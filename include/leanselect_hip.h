@@ -424,6 +424,96 @@ int ls_silu_mul(const void* gate_up, int64_t gu_row_stride, int64_t n_rows, int3
 int ls_embed_scale(const int32_t* ids, int64_t n, const void* table, int64_t vocab,
                    int32_t hidden, float scale, int32_t dtype, void* out, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Decode over a KV cache.  k_cache / v_cache hold [batch][capacity][G][D]
+ * rows and kc_cache [batch][kc_capacity][G][D] (strides in elements, head
+ * stride D); cache_seqlens (int32 [batch], device) counts each sequence's
+ * tokens.  bf16 or fp16.
+ * ------------------------------------------------------------------------ */
+
+/*
+ * Append packed new tokens (k_new / v_new [total_new, G, D], row stride
+ * new_row_stride; sequence b's rows are [cu_seqlens_new[b], cu_seqlens_new[b+1]))
+ * at positions cache_seqlens[b] + i, and, when kc_cache is given, write every
+ * compressed key window the new tokens complete: window w of sequence b is
+ * the mean of key rows [w * kernel_stride, w * kernel_stride + kernel_size)
+ * (float32 sums, one rounding; for 2 x stride windows the two half sums are
+ * added, as ls_compress_k_varlen sums them, so both give the same bits).
+ * cache_seqlens is not advanced: the caller adds the new lengths afterwards.
+ * max_new_windows bounds the new windows of the whole batch (the grid size;
+ * sum over b of ceil(n_new(b) / kernel_stride) + batch always suffices);
+ * cu_windows is int32 [batch + 1] device scratch.  The caller guarantees
+ * cache_seqlens[b] + n_new(b) <= capacity and the windows fit kc_capacity.
+ * Replaces DynamicLayer.update plus InfLLMv2CacheLayer.update_no_compress_k /
+ * update_compress_k (leanselect/models/minicpm.py:1237-1325, called at
+ * 2776-2823 and 2888-2958).
+ */
+int ls_kvcache_append(void* k_cache, void* v_cache, int64_t cache_batch_stride,
+                      int64_t cache_row_stride, const int32_t* cache_seqlens, const void* k_new,
+                      const void* v_new, int64_t new_row_stride, const int32_t* cu_seqlens_new,
+                      int64_t total_new, int32_t batch, int32_t num_kv_heads, int32_t head_dim,
+                      int32_t dtype, void* kc_cache, int64_t kc_batch_stride,
+                      int64_t kc_row_stride, int64_t max_new_windows, int32_t kernel_size,
+                      int32_t kernel_stride, int32_t* cu_windows, void* stream);
+
+/*
+ * Stage-1 page plans for decode rows: q [total_q, H, D] packed by
+ * cu_seqlens_q (row i of sequence b sits at position
+ * cache_seqlens[b] - len_q(b) + i, cache_seqlens counting the rows' own
+ * tokens).  Per row and KV group g:
+ *   score[j] = sum_{h in g} softmax_j(softmax_scale * q_h . kc_j)
+ * over the sequence's n_c = (len - kernel_size) / kernel_stride + 1 compressed
+ * keys (no causal limit), rounded to the query dtype and then to bf16; the
+ * page max-pool with forced sink / local pages of ls_page_maxpool_varlen
+ * (cache_lens = len - len_q); then the `take` = min(topk, out_len) best pages
+ * (ties to the lower page), ascending, ids past the row's own page replaced
+ * by -1.  topk_idx: int32 [G, total_q, take].  max_kc = n_c of the longest
+ * sequence; out_len = ceil((max len_q + max(len - len_q)) / block_size)
+ * (< 65536).  head_dim 128, at most 16 query heads per KV head; kc_cache rows
+ * dense (kc_row_stride = G * D).  Workspace from
+ * ls_decode_select_workspace_size.
+ * Replaces compressed_attention with cache_lens (leanselect/models/minicpm.py:594-705,
+ * called at 2718-2736 with cache_lens = seq_lens_k - 1 from 2509-2512) on
+ * infllmv2_attn_stage1 with causal=False (third_party/infllmv2/paper1.patch:
+ * 1103-1302, 2340-2362) and max_pooling_1d_varlen (paper1.patch:2664-2760).
+ */
+size_t ls_decode_select_workspace_size(int64_t total_q, int32_t batch, int32_t num_kv_heads,
+                                       int64_t max_kc, int64_t out_len);
+int ls_decode_select(const void* q, int64_t q_row_stride, const int32_t* cu_seqlens_q,
+                     int64_t total_q, const void* kc_cache, int64_t kc_batch_stride,
+                     int64_t kc_row_stride, const int32_t* cache_seqlens, int32_t batch,
+                     int64_t max_kc, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int32_t dtype, float softmax_scale, int32_t topk, int32_t block_size,
+                     int32_t kernel_size, int32_t kernel_stride, int32_t init_blocks,
+                     int32_t local_blocks, int64_t out_len, int32_t take, int32_t* topk_idx,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Block-sparse attention of packed query rows over the cache: row i of
+ * sequence b attends the keys of its valid plan ids (topk_idx [G, total_q,
+ * topk], each page once) with j < cache_seqlens[b] (causal = 0) or
+ * j <= cache_seqlens[b] - len_q(b) + i (causal = 1).  out [total_q, H, D] in
+ * the cache dtype, softmax_lse float32 [H, total_q] (natural log; +inf and a
+ * zero row when no key is visible) or NULL.  Split-K over n_splits slices of
+ * each plan (1 <= n_splits <= topk), merged by a second kernel.  head_dim 128,
+ * at most 16 query heads per KV head.  Workspace from
+ * ls_sparse_attn_kvcache_workspace_size.
+ * Replaces infllmv2_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=,
+ * causal=, topk_idx=) (third_party/infllmv2/paper1.patch:2511-2615) and the
+ * decode call infllmv2_attn_varlen_func(..., causal=False, topk_idx=) over the
+ * cached keys (leanselect/models/minicpm.py:3216-3244).
+ */
+size_t ls_sparse_attn_kvcache_workspace_size(int64_t total_q, int32_t num_kv_heads,
+                                             int32_t n_splits);
+int ls_sparse_attn_kvcache(const void* q, int64_t q_row_stride, const int32_t* cu_seqlens_q,
+                           int64_t total_q, const void* k_cache, const void* v_cache,
+                           int64_t cache_batch_stride, int64_t cache_row_stride,
+                           const int32_t* cache_seqlens, int32_t batch, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                           const int32_t* topk_idx, int32_t topk, float softmax_scale,
+                           int32_t causal, int32_t n_splits, void* out, float* softmax_lse,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,6 +75,17 @@ SIGNATURES = {
                _p, _sz, _p]),
     "ls_silu_mul": (_i32, [_p, _i64, _i64, _i32, _i32, _p, _i64, _p]),
     "ls_embed_scale": (_i32, [_p, _i64, _p, _i64, _i32, _f32, _i32, _p, _p]),
+    "ls_kvcache_append": (
+        _i32, [_p, _p, _i64, _i64, _p, _p, _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p, _i64,
+               _i64, _i64, _i32, _i32, _p, _p]),
+    "ls_decode_select_workspace_size": (_sz, [_i64, _i32, _i32, _i64, _i64]),
+    "ls_decode_select": (
+        _i32, [_p, _i64, _p, _i64, _p, _i64, _i64, _p, _i32, _i64, _i32, _i32, _i32, _i32, _f32,
+               _i32, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _p, _p, _sz, _p]),
+    "ls_sparse_attn_kvcache_workspace_size": (_sz, [_i64, _i32, _i32]),
+    "ls_sparse_attn_kvcache": (
+        _i32, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p,
+               _i32, _f32, _i32, _i32, _p, _p, _p, _sz, _p]),
 }
 
 _lib = None

@@ -17,6 +17,13 @@ layer reads q, k and v as strided views of that buffer (no copies).  The
 residual stream is updated in place by the fused add + RMSNorm kernel, whose
 normalised output feeds the next GEMM.
 
+Decoding (``decode_step``) follows the reference's decode branch: each layer
+appends its rotated keys and values to a :class:`LeanSelectKVCache` (with the
+compressed keys they complete), selects pages with the stage-1 selector on the
+compressed-key cache (LeanSelect hands decode selection to it,
+minicpm.py:359-367, 2509-2512, 2718-2736) and attends the cache through those
+pages (minicpm.py:3216-3244 with ``causal=False``).
+
 Weights are random-initialised (no checkpoint is loaded here).  Nothing in this
 module falls back to a non-HIP path: it raises when the library is missing or
 the tensors are not on a GPU.
@@ -30,6 +37,8 @@ import torch
 import torch.nn.functional as F
 
 from . import _hip
+from .cache import LeanSelectKVCache
+from .ops.decode import decode_topk_idx, sparse_attention_kvcache
 from .prefill import leanselect_sparse_prefill
 from .selector import LeanSelectSelector
 
@@ -308,8 +317,12 @@ class MiniCPMLeanSelect:
 
     # -- pieces ----------------------------------------------------------------
     def rope_tables(self, max_pos: int):
+        """Tables covering positions ``< max_pos`` (grown geometrically, so a decode
+        that adds one position per step rebuilds them rarely; a row's values do
+        not depend on the table length)."""
         if self._rope is None or self._rope[0].shape[0] < max_pos:
-            self._rope = rotary_tables(self.cfg.head_dim, max_pos, self.cfg.rope_theta, self.device)
+            n = max(max_pos, 2 * self._rope[0].shape[0]) if self._rope is not None else max_pos
+            self._rope = rotary_tables(self.cfg.head_dim, n, self.cfg.rope_theta, self.device)
         return self._rope
 
     @property
@@ -317,11 +330,14 @@ class MiniCPMLeanSelect:
         return self.cfg.scale_depth / math.sqrt(self.cfg.num_hidden_layers)
 
     def attention(self, li: int, h: torch.Tensor, positions: torch.Tensor, cu_seqlens: torch.Tensor,
-                  cu_host: list[int], return_parts: bool = False):
+                  cu_host: list[int], return_parts: bool = False,
+                  cache: LeanSelectKVCache | None = None):
         """Attention block of layer ``li`` on the normalised input ``h [N, hidden]``.
 
         q/k/v projection (one GEMM), rotary embedding in place, LeanSelect sparse
         prefill on strided views of the projection output, output projection.
+        With ``cache`` (a step open for these tokens) the rotated keys and the
+        values are also written into it.
         """
         cfg, L = self.cfg, self.layers[li]
         H, G, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
@@ -341,6 +357,8 @@ class MiniCPMLeanSelect:
         q = qkv[:, : H * D].view(N, H, D)
         k = qkv[:, H * D: H * D + G * D].view(N, G, D)
         v = qkv[:, H * D + G * D:].view(N, G, D)
+        if cache is not None:
+            cache.update(li, k, v)
         attn, ids = leanselect_sparse_prefill(
             q, k, v, cu_seqlens, L.selector, topk=cfg.topk, local_blocks=cfg.local_blocks,
             init_blocks=cfg.init_blocks, block_size=cfg.block_size, kernel_size=cfg.kernel_size,
@@ -364,14 +382,23 @@ class MiniCPMLeanSelect:
         return torch.cat(parts).to(device)
 
     # -- prefill -----------------------------------------------------------------
+    def new_cache(self, batch: int, capacity: int) -> LeanSelectKVCache:
+        """An empty decode cache for ``batch`` sequences of up to ``capacity`` tokens."""
+        cfg = self.cfg
+        return LeanSelectKVCache(cfg.num_hidden_layers, batch, capacity, cfg.num_key_value_heads,
+                                 cfg.head_dim, dtype=self.dtype, device=self.device,
+                                 kernel_size=cfg.kernel_size, kernel_stride=cfg.kernel_stride)
+
     @torch.no_grad()
     def prefill(self, input_ids: torch.Tensor, cu_seqlens_host: list[int] | None = None,
-                *, layer_hook=None) -> torch.Tensor:
+                *, layer_hook=None, cache: LeanSelectKVCache | None = None) -> torch.Tensor:
         """Last-token logits ``[B, vocab]`` (float32) of packed sequences.
 
         ``input_ids`` int32 ``[N]`` on the GPU; ``cu_seqlens_host`` the packed
         offsets (one sequence of N tokens when omitted).  ``layer_hook(li, x)``,
-        if given, sees the residual stream after each layer.
+        if given, sees the residual stream after each layer.  With an empty
+        ``cache`` (one slot per sequence) every layer's rotated keys, values and
+        compressed keys are kept for ``decode_step``.
         """
         cfg = self.cfg
         N = input_ids.numel()
@@ -383,19 +410,80 @@ class MiniCPMLeanSelect:
             # sequence does not have.
             raise ValueError("every packed sequence must hold at least one token")
         dev = _hip.require_gpu(input_ids)
+        if cache is not None:
+            if cache.batch != len(cu_host) - 1 or any(cache.lengths):
+                raise ValueError("prefill fills an empty cache with one slot per sequence")
+            cache.begin([b - a for a, b in zip(cu_host, cu_host[1:])])
         cu = torch.tensor(cu_host, dtype=torch.int32, device=dev)
         pos = self.positions(cu_host, dev)
         x = embed_scale(input_ids, self.embed, cfg.scale_emb)
         h = rms_layernorm(x, self.layers[0].input_norm, cfg.rms_norm_eps)
         c = self.residual_scale
         for li in range(cfg.num_hidden_layers):
-            o = self.attention(li, h, pos, cu, cu_host)
+            o = self.attention(li, h, pos, cu, cu_host, cache=cache)
             add_rms_layernorm(x, o, c, self.layers[li].post_norm, cfg.rms_norm_eps, out=h)
             d = self.mlp(li, h)
             nxt = self.layers[li + 1].input_norm if li + 1 < cfg.num_hidden_layers else self.final_norm
             add_rms_layernorm(x, d, c, nxt, cfg.rms_norm_eps, out=h)
             if layer_hook is not None:
                 layer_hook(li, x)
+        if cache is not None:
+            cache.end()
         last = torch.tensor([b - 1 for b in cu_host[1:]], device=dev, dtype=torch.long)
         h_last = h.index_select(0, last) / (cfg.hidden_size / cfg.dim_model_base)
         return F.linear(h_last, self.lm_head).float()
+
+    # -- decode ------------------------------------------------------------------
+    def attention_decode(self, li: int, h: torch.Tensor, positions: torch.Tensor,
+                         cache: LeanSelectKVCache, cu_q: torch.Tensor, cu_q_host: list[int]):
+        """Attention block of layer ``li`` for one new token per sequence
+        (``h [B, hidden]``): projection, rotary embedding at each sequence's
+        position, append to the cache, stage-1 page plans on the compressed-key
+        cache, block-sparse attention over the cache, output projection."""
+        cfg, L = self.cfg, self.layers[li]
+        H, G, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        B = h.shape[0]
+        qkv = F.linear(h, L.w_qkv)
+        cos, sin = self.rope_tables(max(cache.lengths_after))
+        rope_inplace(qkv, positions, cos, sin, n_q_heads=H, n_k_heads=G, k_col_offset=H * D,
+                     head_dim=D, check_positions=False)
+        q = qkv[:, : H * D].view(B, H, D)
+        k = qkv[:, H * D: H * D + G * D].view(B, G, D)
+        v = qkv[:, H * D + G * D:].view(B, G, D)
+        cache.update(li, k, v)
+        after = cache.lengths_after
+        ids = decode_topk_idx(q, cache.kc[li], cache.seqlens_after, cu_q, topk=cfg.topk,
+                              init_blocks=cfg.init_blocks, local_blocks=cfg.local_blocks,
+                              block_size=cfg.block_size, kernel_size=cfg.kernel_size,
+                              kernel_stride=cfg.kernel_stride, cache_seqlens_host=after,
+                              cu_seqlens_q_host=cu_q_host)
+        attn = sparse_attention_kvcache(q, cache.k[li], cache.v[li], cache.seqlens_after, ids,
+                                        cu_q, causal=False)
+        return F.linear(attn.view(B, H * D), L.w_o)
+
+    @torch.no_grad()
+    def decode_step(self, input_ids: torch.Tensor, cache: LeanSelectKVCache) -> torch.Tensor:
+        """Logits ``[B, vocab]`` (float32) of one new token per sequence
+        (``input_ids`` int32 ``[B]``), appended to ``cache``."""
+        cfg = self.cfg
+        B = input_ids.numel()
+        if B != cache.batch:
+            raise ValueError(f"one token per cached sequence: {B} ids for {cache.batch} slots")
+        if min(cache.lengths) < 1:
+            raise ValueError("decode_step continues prefilled sequences")
+        dev = _hip.require_gpu(input_ids)
+        pos = torch.tensor(cache.lengths, dtype=torch.int32, device=dev)
+        cu_q_host = list(range(B + 1))
+        cu_q = torch.tensor(cu_q_host, dtype=torch.int32, device=dev)
+        cache.begin([1] * B)
+        x = embed_scale(input_ids, self.embed, cfg.scale_emb)
+        h = rms_layernorm(x, self.layers[0].input_norm, cfg.rms_norm_eps)
+        c = self.residual_scale
+        for li in range(cfg.num_hidden_layers):
+            o = self.attention_decode(li, h, pos, cache, cu_q, cu_q_host)
+            add_rms_layernorm(x, o, c, self.layers[li].post_norm, cfg.rms_norm_eps, out=h)
+            d = self.mlp(li, h)
+            nxt = self.layers[li + 1].input_norm if li + 1 < cfg.num_hidden_layers else self.final_norm
+            add_rms_layernorm(x, d, c, nxt, cfg.rms_norm_eps, out=h)
+        cache.end()
+        return F.linear(h / (cfg.hidden_size / cfg.dim_model_base), self.lm_head).float()

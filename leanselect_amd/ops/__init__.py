@@ -4,6 +4,7 @@ from .compress import CompressK, compress_k
 from .select import leanselect_prefill_topk_idx, select_take
 from .cis_pooling import nosa_mean_pooling
 from .nosa import max_pooling_1d_varlen, nosa_prefill_topk_idx, nosa_sparse_attention
+from .decode import decode_topk_idx, kvcache_append, sparse_attention_kvcache
 from . import profiling
 
 __all__ = [
@@ -17,5 +18,8 @@ __all__ = [
     "max_pooling_1d_varlen",
     "nosa_prefill_topk_idx",
     "nosa_sparse_attention",
+    "kvcache_append",
+    "decode_topk_idx",
+    "sparse_attention_kvcache",
     "profiling",
 ]

@@ -13,3 +13,4 @@ from .check import *  # noqa: F401,F403
 from .nosa_oracle import *  # noqa: F401,F403
 from .minicpm_oracle import *  # noqa: F401,F403
 from .reference_path import *  # noqa: F401,F403
+from .decode_oracle import *  # noqa: F401,F403
