@@ -216,7 +216,7 @@ int ls_nosa_cis_pages_launch(const void* cis, int64_t cis_rs, int cis_dtype, con
 // are held as keys in NS register slots of 64 lanes (page p = 64 s + lane).
 //   stage 1: qk keys (forced pages +inf, pages p <= A_b / 4 from the page-score
 //            scratch, others -inf); the qk_select best pages (ties to the lower
-//            page) form the shortlist;
+//            page) form the shortlist S;
 //   stage 2: CIS keys (shortlisted pages +inf; other pages after the row's
 //            q_idx -inf; forced pages +inf; others the sequence's CIS page
 //            score, -inf past A_b / 4); the `take` best pages, emitted
@@ -224,6 +224,16 @@ int ls_nosa_cis_pages_launch(const void* cis, int64_t cis_rs, int cis_dtype, con
 // off_bq = t_rel / block_size places the forced pages; q_idx =
 // (t_rel + max_seqlen_q - len_q(b)) / block_size is aligned to the longest
 // sequence (nosa.py:1175-1189).
+//
+// Stage 2 does not rank each row's pages again.  Outside S a row's stage-2
+// key depends only on (off_bq, q_idx) and the sequence's CIS page scores, so
+// the rows of one 64-row query block share it: with K0 the row-independent
+// key, the stage-2 choice is S (all +inf; the forced pages are in S, since
+// stage 1 puts them first and qk_select covers them) plus the first
+// take - |S| pages of the block's order of K0 (key descending, page
+// ascending) that are not in S.  ls_nosa_cis_rank_kernel writes the first
+// take + qk_select pages of that order once per block and q_idx value, which
+// covers every row (at most |S| of them are skipped).
 // ---------------------------------------------------------------------------
 // Threshold T such that #{key > T} < kk <= #{key >= T} (bisection over the
 // key bits with ballot counts; keys of inactive lanes are 0).
@@ -250,19 +260,16 @@ __device__ __forceinline__ void ls_mark_topk(const uint32_t (&key)[NS], uint32_t
 // stage 2 uses the top 16 bits of the float32 keys when the CIS page scores
 // are bf16 values (CIS32 off: their low 16 bits are zero), so each bisection
 // runs over 16 bits instead of 32.
-template <int NS, bool KEY32, bool CIS32>
+template <int NS, bool KEY32>
 __device__ __forceinline__ void ls_nosa_topk_row(
-    const void* __restrict__ P, int64_t prow, const float* __restrict__ cpg_seq, int n_scored,
-    int out_len, int off_bq, int q_idx, int init_blocks, int local_blocks, int qk_select,
-    int take, uint32_t pinf1, uint32_t ninf1, int lane, int32_t* __restrict__ orow,
-    uint32_t* __restrict__ scr, const float* __restrict__ cpg_lds) {
+    const void* __restrict__ P, int64_t prow, int n_scored, int out_len, int off_bq, int q_idx,
+    int init_blocks, int local_blocks, int qk_select, int take, uint32_t pinf1, uint32_t ninf1,
+    int lane, int32_t* __restrict__ orow, uint32_t* __restrict__ scr,
+    const int32_t* __restrict__ order, int n_order) {
   constexpr int NW = (NS + 31) / 32;
   // Every +inf (forced or shortlisted) and every -inf is one key, so ties among
   // them go to the lower page as in a stable sort.  Stage 1 keys come from the
-  // page-score dtype (pinf1 / ninf1), stage 2 keys from float32.
-  constexpr int SH2 = CIS32 ? 0 : 16;
-  const uint32_t pinf2 = ls_order_key32(0x7f800000u) >> SH2;
-  const uint32_t ninf2 = ls_order_key32(0xff800000u) >> SH2;
+  // page-score dtype (pinf1 / ninf1).
   uint32_t key[NS];
   // Stage 1 keys.
 #pragma unroll
@@ -290,76 +297,210 @@ __device__ __forceinline__ void ls_nosa_topk_row(
   for (int i = 0; i < NW; ++i) shortlist[i] = 0u;
   ls_mark_topk<NS>(key, ls_kth_key_row<NS, KEY32 ? 32 : 16>(key, qk_select, scr, lane), qk_select,
                    shortlist);
-  // Stage 2 keys (the CIS page scores from the workgroup's LDS copy when its
-  // rows share a sequence and group).
+  // Stage 2.  The wave's scratch (free once stage 1 is done) becomes the
+  // chosen-page bitmap: S first, then the block order's first take - |S|
+  // pages outside S.
+  const int n_words = (out_len + 31) >> 5;
+  for (int i = lane; i < n_words; i += 64) scr[i] = 0u;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int n_s = 0;
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    const int p = s * 64 + lane;
-    const float cis_lds = cpg_lds ? cpg_lds[p] : 0.f;
-    uint32_t k;
-    // The reference's order: pooled CIS scores with the forced overlay, then
-    // pages after q_idx -inf, then the shortlist +inf.
-    if (p >= out_len) k = 0u;
-    else if ((shortlist[s >> 5] >> (s & 31)) & 1u) k = pinf2;
-    else if (p > q_idx) k = ninf2;
-    else if (p < init_blocks || (off_bq - local_blocks <= p && p <= off_bq)) k = pinf2;
-    else if (p >= n_scored) k = ninf2;
-    else k = ls_order_key32(__builtin_bit_cast(uint32_t, cpg_lds ? cis_lds : cpg_seq[p])) >> SH2;
-    key[s] = k;
+    const uint64_t m = __ballot((shortlist[s >> 5] >> (s & 31)) & 1u);
+    if (lane < 2) scr[2 * s + lane] = lane ? (uint32_t)(m >> 32) : (uint32_t)m;
+    n_s += __popcll(m);
   }
-  uint32_t chosen[NW];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (n_s > take) {
+    // More shortlisted pages than the budget (topk below init + local +
+    // select): all are +inf, so the lowest `take` of them are chosen.
+    int before = 0;
+    for (int w0 = 0; w0 < n_words; w0 += 64) {
+      const int wi = w0 + lane;
+      uint32_t word = wi < n_words ? scr[wi] : 0u;
+      const int cnt = __popc(word);
+      int x = cnt;
 #pragma unroll
-  for (int i = 0; i < NW; ++i) chosen[i] = 0u;
-  ls_mark_topk<NS>(key, ls_kth_key_row<NS, CIS32 ? 32 : 16>(key, take, scr, lane), take, chosen);
+      for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, LS_WAVE);
+        if (lane >= d) x += y;
+      }
+      const int pre = before + x - cnt;
+      if (pre >= take) {
+        word = 0u;
+      } else if (pre + cnt > take) {  // keep the word's lowest take - pre pages
+        uint32_t kept = 0u, wcopy = word;
+        for (int c = 0; c < take - pre; ++c) {
+          const uint32_t low = wcopy & (0u - wcopy);
+          kept |= low;
+          wcopy ^= low;
+        }
+        word = kept;
+      }
+      if (wi < n_words) scr[wi] = word;
+      before += __shfl(x, 63, LS_WAVE);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  const int need = take - n_s;
+  int picked = 0;
+  for (int i0 = 0; i0 < n_order && picked < need; i0 += 64) {
+    const int i = i0 + lane;
+    const int page = i < n_order ? order[i] : -1;
+    const bool avail = page >= 0 && !((scr[page >> 5] >> (page & 31)) & 1u);
+    const uint64_t m = __ballot(avail);
+    if (avail && picked + ls_lanes_below(m) < need) atomicOr(&scr[page >> 5], 1u << (page & 31));
+    picked += __popcll(m);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   // Emission: chosen pages <= q_idx in ascending order, then -1.
   int out_pos = 0;
+  for (int w0 = 0; w0 < n_words; w0 += 64) {
+    const int wi = w0 + lane;
+    uint32_t word = wi < n_words ? scr[wi] : 0u;
+    if (32 * wi > q_idx) word = 0u;
+    else if (32 * wi + 31 > q_idx) word &= (2u << (q_idx & 31)) - 1u;
+    const int cnt = __popc(word);
+    int x = cnt;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const int p = s * 64 + lane;
-    const bool emit = ((chosen[s >> 5] >> (s & 31)) & 1u) && p <= q_idx;
-    const uint64_t m = __ballot(emit);
-    const int pos = out_pos + ls_lanes_below(m);
-    if (emit && pos < take) orow[pos] = p;  // at most take by construction
-    out_pos += __popcll(m);
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(x, d, LS_WAVE);
+      if (lane >= d) x += y;
+    }
+    int pos = out_pos + x - cnt;
+    while (word) {
+      const int bit = __builtin_ctz(word);
+      word &= word - 1u;
+      if (pos < take) orow[pos] = 32 * wi + bit;  // at most take by construction
+      ++pos;
+    }
+    out_pos += __shfl(x, 63, LS_WAVE);
   }
   for (int i = out_pos + lane; i < take; i += 64) orow[i] = -1;
 }
 
-template <int KPL, bool KEY32, bool CIS32>
+// The block's stage-2 order.  One wave per (64-row query block, group, q_idx
+// variant): the rows of block j of sequence b have off_bq = j and q_idx = qa
+// or qa + 1, qa = (64 j + max_seqlen_q - len_q(b)) / 64.  Keys K0 of pages
+// p < out_len: -inf after q_idx, +inf forced, -inf without a CIS page score
+// (p > A_b / 4), else the float32 CIS page score; the n_order best (ties to
+// the lower page) are written best first to order[((g * n_blk + blk) * 2 + v)
+// * n_order + i] (entries past out_len pages stay -1).
+template <int NS>
+__device__ __forceinline__ void ls_nosa_rank_block(const float* __restrict__ cpg_seq, int n_scored,
+                                                   int out_len, int off_bq, int q_idx,
+                                                   int init_blocks, int local_blocks, int n_order,
+                                                   int lane, int32_t* __restrict__ out,
+                                                   uint32_t* __restrict__ scr,
+                                                   uint32_t* __restrict__ s_key,
+                                                   int32_t* __restrict__ s_page) {
+  constexpr int NW = (NS + 31) / 32;
+  const uint32_t pinf = ls_order_key32(0x7f800000u), ninf = ls_order_key32(0xff800000u);
+  uint32_t key[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int p = s * 64 + lane;
+    uint32_t k;
+    if (p >= out_len) k = 0u;
+    else if (p > q_idx) k = ninf;
+    else if (p < init_blocks || (off_bq - local_blocks <= p && p <= off_bq)) k = pinf;
+    else if (p >= n_scored) k = ninf;
+    else k = ls_order_key32(__builtin_bit_cast(uint32_t, cpg_seq[p]));
+    key[s] = k;
+  }
+  const int kk = n_order < out_len ? n_order : out_len;
+  uint32_t sel[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) sel[i] = 0u;
+  ls_mark_topk<NS>(key, ls_kth_key_row<NS, 32>(key, kk, scr, lane), kk, sel);
+  // The chosen (key, page) pairs in page order, then each one's rank.
+  int n = 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool on = (sel[s >> 5] >> (s & 31)) & 1u;
+    const uint64_t m = __ballot(on);
+    if (on) {
+      const int pos = n + ls_lanes_below(m);
+      s_key[pos] = key[s];
+      s_page[pos] = s * 64 + lane;
+    }
+    n += __popcll(m);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (int i = lane; i < n; i += 64) {
+    const uint32_t ki = s_key[i];
+    const int pi = s_page[i];
+    int rank = 0;
+    for (int j = 0; j < n; ++j) {
+      const uint32_t kj = s_key[j];
+      rank += (kj > ki || (kj == ki && s_page[j] < pi)) ? 1 : 0;
+    }
+    out[rank] = pi;
+  }
+  for (int i = n + lane; i < n_order; i += 64) out[i] = -1;
+}
+
+#define LS_NOSA_MAX_ORDER LS_NOSA_ORDER_STRIDE  // bound on take + qk_select
+
+template <int KPL>
+__global__ __launch_bounds__(64) void ls_nosa_cis_rank_kernel(
+    const float* __restrict__ cpg, int64_t cpg_g_stride, const int32_t* __restrict__ pg_off,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_a,
+    const int32_t* __restrict__ blk_off, int batch, int64_t n_blk, int max_seqlen_q, int out_len,
+    int init_blocks, int local_blocks, int block_size, int n_order, int32_t* __restrict__ order) {
+  __shared__ uint32_t s_scr[256];
+  __shared__ uint32_t s_key[LS_NOSA_MAX_ORDER];
+  __shared__ int32_t s_page[LS_NOSA_MAX_ORDER];
+  const int64_t blk = blockIdx.x;
+  const int g = blockIdx.y, v = blockIdx.z;
+  const int lane = threadIdx.x;
+  if (blk >= blk_off[batch]) return;
+  const int b = ls_find_segment(blk_off, batch, blk);
+  const int j = (int)(blk - blk_off[b]);
+  const int lq = cu_q[b + 1] - cu_q[b];
+  const int qa = (block_size * j + max_seqlen_q - lq) / block_size;
+  const int t_last = min(block_size * j + block_size - 1, lq - 1);
+  int32_t* out = order + (((int64_t)g * n_blk + blk) * 2 + v) * n_order;
+  if (v == 1 && (t_last + max_seqlen_q - lq) / block_size == qa) return;  // one q_idx only
+  const int A = cu_a[b + 1] - cu_a[b];
+  const int n_scored = min(A > 0 ? A / 4 + 1 : 0, out_len);
+  const float* cpg_seq = cpg + (int64_t)g * cpg_g_stride + pg_off[b];
+  const int n_slots = (out_len + 63) >> 6;
+#define LS_RANK(NSV) ls_nosa_rank_block<NSV>(cpg_seq, n_scored, out_len, j, qa + v, init_blocks, \
+                                             local_blocks, n_order, lane, out, s_scr, s_key, s_page)
+  if (n_slots <= 1) return LS_RANK(1);
+  if (n_slots <= 4 || KPL <= 4) return LS_RANK(KPL < 4 ? KPL : 4);
+  if (n_slots <= 16 || KPL <= 16) return LS_RANK(KPL < 16 ? KPL : 16);
+  if (n_slots <= 32 || KPL <= 32) return LS_RANK(KPL < 32 ? KPL : 32);
+  if (n_slots <= 64 || KPL <= 64) return LS_RANK(KPL < 64 ? KPL : 64);
+  return LS_RANK(KPL);
+#undef LS_RANK
+}
+
+template <int KPL, bool KEY32>
 __global__ __launch_bounds__(256) void ls_nosa_topk_kernel(
-    const void* __restrict__ P, int64_t p_stride, const float* __restrict__ cpg, int64_t cpg_g_stride,
-    const int32_t* __restrict__ pg_off, const int32_t* __restrict__ cu_q,
-    const int32_t* __restrict__ cu_a, int batch, int64_t total_q, int G, int max_seqlen_q,
-    int out_len, int init_blocks, int local_blocks, int qk_select, int take, int block_size,
-    uint32_t pinf1, uint32_t ninf1, int32_t* __restrict__ topk_idx) {
-  __shared__ uint32_t s_scr[4][256];  // per-wave gather space of the k-th key search
-  // The CIS page scores of the workgroup's sequence and group, when its four
-  // rows share them (all but the workgroups that straddle a boundary).
-  __shared__ __align__(16) float s_cpg[KPL * 64];
+    const void* __restrict__ P, int64_t p_stride, const int32_t* __restrict__ cu_q,
+    const int32_t* __restrict__ cu_a, const int32_t* __restrict__ blk_off, int batch,
+    int64_t total_q, int G, int max_seqlen_q, int out_len, int init_blocks, int local_blocks,
+    int qk_select, int take, int block_size, uint32_t pinf1, uint32_t ninf1,
+    const int32_t* __restrict__ order, int64_t n_blk, int n_order, int32_t* __restrict__ topk_idx) {
+  __shared__ uint32_t s_scr[4][256];  // per-wave k-th key scratch, then the chosen-page bitmap
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t n_rows = (int64_t)G * total_q;
-  const int64_t row0 = (int64_t)blockIdx.x * 4;
-  const int64_t row_l = min(row0 + 3, n_rows - 1);
-  const int g0 = (int)(row0 / total_q), gl = (int)(row_l / total_q);
-  const int b0 = ls_find_segment(cu_q, batch, row0 - (int64_t)g0 * total_q);
-  const int bl = ls_find_segment(cu_q, batch, row_l - (int64_t)gl * total_q);
-  const bool shared_cis = g0 == gl && b0 == bl;
-  if (shared_cis) {
-    const int A0 = cu_a[b0 + 1] - cu_a[b0];
-    const int n_sc = min(A0 > 0 ? A0 / 4 + 1 : 0, out_len);
-    const int last = n_sc > 0 ? n_sc - 1 : 0;
-    const float* cs = cpg + (int64_t)g0 * cpg_g_stride + pg_off[b0];
-    const uint32_t base = (uint32_t)(uintptr_t)(ls_lds_void*)s_cpg;
-    for (int sl = wv; sl < (n_sc + 63) / 64; sl += 4)
-      ls_dma4(cs, 4u * (uint32_t)min(sl * 64 + lane, last), base + 256u * (uint32_t)sl);
-    LS_WAIT_VMCNT(0);
-  }
-  __syncthreads();
-  const int64_t row = row0 + wv;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wv;
   if (row >= n_rows) return;
   uint32_t* const scr = s_scr[wv];
-  const float* const cpg_lds = shared_cis ? s_cpg : nullptr;
   const int g = (int)(row / total_q);
   const int64_t t = row - (int64_t)g * total_q;
   const int b = ls_find_segment(cu_q, batch, t);
@@ -370,30 +511,49 @@ __global__ __launch_bounds__(256) void ls_nosa_topk_kernel(
   if (n_scored > out_len) n_scored = out_len;
   const int off_bq = t_rel / block_size;
   const int q_idx = (t_rel + max_seqlen_q - lq) / block_size;
-  const float* cpg_seq = cpg + (int64_t)g * cpg_g_stride + pg_off[b];
+  const int qa = (block_size * off_bq + max_seqlen_q - lq) / block_size;
+  const int32_t* ord = order + (((int64_t)g * n_blk + blk_off[b] + off_bq) * 2 + (q_idx - qa)) * n_order;
   int32_t* orow = topk_idx + row * take;
   const int64_t prow = row * p_stride;
   const int n_slots = (out_len + 63) >> 6;
-  if (n_slots <= 1) return ls_nosa_topk_row<1, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
-  if (n_slots <= 2) return ls_nosa_topk_row<2, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
-  if (n_slots <= 4 || KPL <= 4) return ls_nosa_topk_row<(KPL < 4 ? KPL : 4), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
-  if (n_slots <= 8 || KPL <= 8) return ls_nosa_topk_row<(KPL < 8 ? KPL : 8), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
-  if (n_slots <= 16 || KPL <= 16) return ls_nosa_topk_row<(KPL < 16 ? KPL : 16), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
-  if (n_slots <= 32 || KPL <= 32) return ls_nosa_topk_row<(KPL < 32 ? KPL : 32), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
-  if (n_slots <= 64 || KPL <= 64) return ls_nosa_topk_row<(KPL < 64 ? KPL : 64), KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
-  return ls_nosa_topk_row<KPL, KEY32, CIS32>(P, prow, cpg_seq, n_scored, out_len, off_bq, q_idx, init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, cpg_lds);
+  const int n_ord = n_order < out_len ? n_order : out_len;
+#define LS_ROW(NSV) ls_nosa_topk_row<NSV, KEY32>(P, prow, n_scored, out_len, off_bq, q_idx, \
+    init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, ord, n_ord)
+  if (n_slots <= 1) return LS_ROW(1);
+  if (n_slots <= 2) return LS_ROW(2);
+  if (n_slots <= 4 || KPL <= 4) return LS_ROW(KPL < 4 ? KPL : 4);
+  if (n_slots <= 8 || KPL <= 8) return LS_ROW(KPL < 8 ? KPL : 8);
+  if (n_slots <= 16 || KPL <= 16) return LS_ROW(KPL < 16 ? KPL : 16);
+  if (n_slots <= 32 || KPL <= 32) return LS_ROW(KPL < 32 ? KPL : 32);
+  if (n_slots <= 64 || KPL <= 64) return LS_ROW(KPL < 64 ? KPL : 64);
+  return LS_ROW(KPL);
+#undef LS_ROW
 }
 
-template <bool KEY32, bool CIS32>
-static int launch_nosa_topk_k(int out_len, dim3 grid, hipStream_t s, const void* P, int64_t ps,
+size_t ls_nosa_order_bytes(int64_t n_blk, int G, int n_order) {
+  return (size_t)G * n_blk * 2 * n_order * 4;
+}
+
+template <bool KEY32>
+static int launch_nosa_topk_k(int out_len, hipStream_t s, const void* P, int64_t ps,
                               const float* cpg, int64_t cs, const int32_t* pg_off,
-                              const int32_t* cu_q, const int32_t* cu_a, int batch, int64_t total_q,
-                              int G, int max_q, int init, int local, int qk_select, int take,
-                              int bs, uint32_t pinf1, uint32_t ninf1, int32_t* out) {
+                              const int32_t* cu_q, const int32_t* cu_a, const int32_t* blk_off,
+                              int64_t n_blk, int batch, int64_t total_q, int G, int max_q,
+                              int init, int local, int qk_select, int take, int bs,
+                              uint32_t pinf1, uint32_t ninf1, int32_t* order, int32_t* out) {
+  const int n_order = take + qk_select;
+  const dim3 rgrid((unsigned)n_blk, G, 2);
+  const dim3 grid((unsigned)(((int64_t)G * total_q + 3) / 4));
 #define LS_NOSA_TOPK(K)                                                                          \
-  hipLaunchKernelGGL((ls_nosa_topk_kernel<K, KEY32, CIS32>), grid, dim3(256), 0, s, P, ps, cpg, cs,    \
-                     pg_off, cu_q, cu_a, batch, total_q, G, max_q, out_len, init, local,       \
-                     qk_select, take, bs, pinf1, ninf1, out)
+  do {                                                                                         \
+    hipLaunchKernelGGL((ls_nosa_cis_rank_kernel<K>), rgrid, dim3(64), 0, s, cpg, cs, pg_off,   \
+                       cu_q, cu_a, blk_off, batch, n_blk, max_q, out_len, init, local, bs,    \
+                       n_order, order);                                                        \
+    if (int rc = ls_check_launch("ls_nosa_cis_rank_kernel")) return rc;                       \
+    hipLaunchKernelGGL((ls_nosa_topk_kernel<K, KEY32>), grid, dim3(256), 0, s, P, ps, cu_q,   \
+                       cu_a, blk_off, batch, total_q, G, max_q, out_len, init, local,         \
+                       qk_select, take, bs, pinf1, ninf1, order, n_blk, n_order, out);        \
+  } while (0)
   if (out_len <= 256) LS_NOSA_TOPK(4);
   else if (out_len <= 1024) LS_NOSA_TOPK(16);
   else if (out_len <= 2048) LS_NOSA_TOPK(32);
@@ -404,25 +564,26 @@ static int launch_nosa_topk_k(int out_len, dim3 grid, hipStream_t s, const void*
   return ls_check_launch("ls_nosa_topk_kernel");
 }
 
-int ls_nosa_topk_launch(int p_dtype, int cis_dtype, int out_len, const void* P, int64_t p_stride, const float* cpg,
+int ls_nosa_topk_launch(int p_dtype, int out_len, const void* P, int64_t p_stride, const float* cpg,
                         int64_t cpg_g_stride, const int32_t* pg_off, const int32_t* cu_q,
-                        const int32_t* cu_a, int batch, int64_t total_q, int G, int max_seqlen_q,
-                        int init_blocks, int local_blocks, int qk_select, int take,
-                        int block_size, int32_t* topk_idx, hipStream_t s) {
+                        const int32_t* cu_a, const int32_t* blk_off, int64_t n_blk, int batch,
+                        int64_t total_q, int G, int max_seqlen_q, int init_blocks,
+                        int local_blocks, int qk_select, int take, int block_size,
+                        int32_t* order, int32_t* topk_idx, hipStream_t s) {
   if (total_q == 0 || G == 0 || take == 0) return LS_OK;
-  const dim3 grid((unsigned)(((int64_t)G * total_q + 3) / 4));
-  const bool cis16 = cis_dtype == LS_BF16;
+  if (take + qk_select > LS_NOSA_MAX_ORDER)
+    return ls_fail(LS_ERR_UNSUPPORTED, "NOSA selection: topk + init + local + select blocks "
+                   "above %d", LS_NOSA_MAX_ORDER);
 #define LS_NOSA_TOPK_ARGS                                                                      \
-  out_len, grid, s, P, p_stride, cpg, cpg_g_stride, pg_off, cu_q, cu_a, batch, total_q, G,   \
-      max_seqlen_q, init_blocks, local_blocks, qk_select, take, block_size, pinf, ninf, topk_idx
+  out_len, s, P, p_stride, cpg, cpg_g_stride, pg_off, cu_q, cu_a, blk_off, n_blk, batch,     \
+      total_q, G, max_seqlen_q, init_blocks, local_blocks, qk_select, take, block_size, pinf, \
+      ninf, order, topk_idx
   if (p_dtype == LS_F32) {
     const uint32_t pinf = ls_order_key32(0x7f800000u), ninf = ls_order_key32(0xff800000u);
-    return cis16 ? launch_nosa_topk_k<true, false>(LS_NOSA_TOPK_ARGS)
-                 : launch_nosa_topk_k<true, true>(LS_NOSA_TOPK_ARGS);
+    return launch_nosa_topk_k<true>(LS_NOSA_TOPK_ARGS);
   }
   const uint32_t pinf = ls_order_key16(p_dtype == LS_BF16 ? 0x7f80u : 0x7c00u);
   const uint32_t ninf = ls_order_key16(p_dtype == LS_BF16 ? 0xff80u : 0xfc00u);
-  return cis16 ? launch_nosa_topk_k<false, false>(LS_NOSA_TOPK_ARGS)
-               : launch_nosa_topk_k<false, true>(LS_NOSA_TOPK_ARGS);
+  return launch_nosa_topk_k<false>(LS_NOSA_TOPK_ARGS);
 #undef LS_NOSA_TOPK_ARGS
 }

@@ -889,8 +889,8 @@ WsLayout ws_layout(int64_t total_q, int64_t total_atoms, int batch, int H, int G
 // scores cpg[g][*] (at most total_atoms / 4 + batch pages per group).
 struct NosaWsLayout {
   WsLayout L;
-  size_t pg, cpg, total;
-  int64_t cpg_stride;
+  size_t pg, cpg, order, total;
+  int64_t cpg_stride, n_blk;
 };
 
 NosaWsLayout nosa_ws_layout(int64_t total_q, int64_t total_atoms, int batch, int H, int G, int D,
@@ -901,6 +901,9 @@ NosaWsLayout nosa_ws_layout(int64_t total_q, int64_t total_atoms, int batch, int
   N.pg = off; off += ls_align256((size_t)(batch + 1) * 4);
   N.cpg_stride = (total_atoms / 4 + batch + 63) & ~(int64_t)63;
   N.cpg = off; off += ls_align256((size_t)G * N.cpg_stride * 4);
+  // The query blocks' stage-2 page orders (64-row blocks: block_size 64).
+  N.n_blk = (total_q + 63) / 64 + batch;
+  N.order = off; off += ls_align256(ls_nosa_order_bytes(N.n_blk, G, LS_NOSA_ORDER_STRIDE));
   N.total = off;
   return N;
 }
@@ -1370,7 +1373,8 @@ extern "C" int ls_nosa_select_prefill(
   if ((rc = ls_nosa_cis_pages_launch(cis, cis_row_stride, cis_dtype, cu_seqlens_k, cu_seqlens_kc,
                                      batch, total_atoms, G, pg_off, cpg, N.cpg_stride, s)))
     return rc;
-  return ls_nosa_topk_launch(dtype, cis_dtype, out_len, ws + L.p, L.p_stride, cpg, N.cpg_stride, pg_off,
-                             cu_seqlens_q, cu_seqlens_kc, batch, total_q, G, max_seqlen_q,
-                             init_blocks, local_blocks, qk_select, take, block_size, topk_idx, s);
+  return ls_nosa_topk_launch(dtype, out_len, ws + L.p, L.p_stride, cpg, N.cpg_stride, pg_off,
+                             cu_seqlens_q, cu_seqlens_kc, blk, N.n_blk, batch, total_q, G,
+                             max_seqlen_q, init_blocks, local_blocks, qk_select, take, block_size,
+                             (int32_t*)(ws + N.order), topk_idx, s);
 }
