@@ -18,9 +18,15 @@ projections, HIP kernels for everything else.  Its line reports seconds per
 prefill and a per-stage breakdown of one layer.
 
 ``--variant nosa`` times the NOSA layer instead (budget 96 pages = 1 sink +
-16 local + 79 chosen, shortlist 41, CIS-biased attention) on the same shapes;
-its CPU baseline is not run (the oracle's broadcast CIS pooling alone would
-need ~17 GB at 128K).
+16 local + 79 chosen, shortlist 41, CIS-biased attention) on the same shapes,
+with the NOSA path restated on the host for its CPU baseline.
+
+``--workload minicpm41_8b_decode_128k`` (and ``..._b16``) times one decode
+step of one attention layer over a 128K-token KV cache per sequence: the
+cache append with its compressed keys, stage-1 page plans and split-K
+block-sparse attention over the cache (the reference's decode path), in
+microseconds per layer; the roofline is the HBM rate of the attention's page
+reads.
 """
 from __future__ import annotations
 
@@ -47,6 +53,8 @@ WORKLOADS = {
     "minicpm41_8b_prefill_32k": dict(seq_lens=(32768,), model=True),
     "minicpm41_8b_prefill_64k": dict(seq_lens=(65536,), model=True),
     "minicpm41_8b_prefill_128k": dict(seq_lens=(131072,), model=True),
+    "minicpm41_8b_decode_128k": dict(seq_lens=(131072,), decode=True, batch=1),
+    "minicpm41_8b_decode_128k_b16": dict(seq_lens=(131072,), decode=True, batch=16),
 }
 # Published whole-model LeanSelect prefill times of the reference (H200, real
 # weights, budget 96 pages with 32 local blocks, LongRoPE, median of 10 runs;
@@ -266,6 +274,177 @@ def cpu_baseline_nosa(case, cis, n_rows: int, threads: int, runs: int = 3) -> di
     }
 
 
+def decode_bench(args, dev) -> None:
+    """One decode step of one MiniCPM4.1-8B attention layer over a KV cache."""
+    from leanselect_amd.ops import decode_topk_idx, kvcache_append, sparse_attention_kvcache
+    from leanselect_amd.ops.decode import n_windows
+
+    wl = WORKLOADS[args.workload]
+    B, ctx = wl["batch"], wl["seq_lens"][0]
+    H, G, D, topk, local, init = 32, 2, 128, 64, 4, 1
+    n_steps = args.warmup + args.steps
+    cap = -(-(ctx + n_steps + 1) // 64) * 64
+    bf = torch.bfloat16
+    print(f"[bench] filling a {B} x {ctx}-token cache ...", file=sys.stderr, flush=True)
+    g = torch.Generator(device=dev).manual_seed(0)
+    k = torch.empty(B, cap, G, D, dtype=bf, device=dev)
+    v = torch.empty_like(k)
+    kc = torch.empty(B, n_windows(cap), G, D, dtype=bf, device=dev)
+    zeros = torch.zeros(B, dtype=torch.int32, device=dev)
+    for b in range(B):  # one sequence at a time keeps the fill's temporaries small
+        kp = torch.randn(ctx, G, D, generator=g, device=dev).to(bf)
+        vp = torch.randn(ctx, G, D, generator=g, device=dev).to(bf)
+        one = torch.zeros(B + 1, dtype=torch.int32, device=dev)
+        one[b + 1:] = ctx
+        kvcache_append(k, v, zeros, kp, vp, one, kc_cache=kc, cache_seqlens_host=[0] * B,
+                       cu_seqlens_new_host=[0] * (b + 1) + [ctx] * (B - b))
+        del kp, vp
+    q = torch.randn(n_steps, B, H, D, generator=g, device=dev).to(bf)
+    kn = torch.randn(n_steps, B, G, D, generator=g, device=dev).to(bf)
+    vn = torch.randn(n_steps, B, G, D, generator=g, device=dev).to(bf)
+    cu_q_host = list(range(B + 1))
+    cu_q = torch.tensor(cu_q_host, dtype=torch.int32, device=dev)
+    lens = [ctx] * B
+
+    def step(i, lens):
+        after = [x + 1 for x in lens]
+        before_t = torch.tensor(lens, dtype=torch.int32, device=dev)
+        after_t = torch.tensor(after, dtype=torch.int32, device=dev)
+        kvcache_append(k, v, before_t, kn[i], vn[i], cu_q, kc_cache=kc, cache_seqlens_host=lens,
+                       cu_seqlens_new_host=cu_q_host)
+        ids = decode_topk_idx(q[i], kc, after_t, cu_q, topk=topk, init_blocks=init,
+                              local_blocks=local, cache_seqlens_host=after,
+                              cu_seqlens_q_host=cu_q_host)
+        out = sparse_attention_kvcache(q[i], k, v, after_t, ids, cu_q)
+        return after, ids, out
+
+    for i in range(args.warmup):
+        lens, ids, out = step(i, lens)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.warmup, n_steps):
+        lens, ids, out = step(i, lens)
+    torch.cuda.synchronize()
+    us_step = 1e6 * (time.perf_counter() - t0) / args.steps
+    # Per-stage kernel time on the final lengths (HIP events on the launch stream).
+    it = args.kernel_iters
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=dev)
+    prev_t = lens_t - 1
+    prev = [x - 1 for x in lens]
+    us_append = 1e3 * _event_ms(lambda: kvcache_append(
+        k, v, prev_t, kn[-1], vn[-1], cu_q, kc_cache=kc, cache_seqlens_host=prev,
+        cu_seqlens_new_host=cu_q_host), it)
+    us_select = 1e3 * _event_ms(lambda: decode_topk_idx(
+        q[-1], kc, lens_t, cu_q, topk=topk, init_blocks=init, local_blocks=local,
+        cache_seqlens_host=lens, cu_seqlens_q_host=cu_q_host), it)
+    us_attn = 1e3 * _event_ms(lambda: sparse_attention_kvcache(q[-1], k, v, lens_t, ids, cu_q), it)
+    # The same three calls captured in HIP graphs and replayed: the GPU time of
+    # a step without the host's per-call launch overhead (a serving loop would
+    # replay them the same way).
+    graph_us = {}
+    try:
+        calls = {
+            "append_and_compress": lambda: kvcache_append(
+                k, v, prev_t, kn[-1], vn[-1], cu_q, kc_cache=kc, cache_seqlens_host=prev,
+                cu_seqlens_new_host=cu_q_host),
+            "select": lambda: decode_topk_idx(
+                q[-1], kc, lens_t, cu_q, topk=topk, init_blocks=init, local_blocks=local,
+                cache_seqlens_host=lens, cu_seqlens_q_host=cu_q_host),
+            "sparse_attention": lambda: sparse_attention_kvcache(q[-1], k, v, lens_t, ids, cu_q),
+        }
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for fn in calls.values():
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graphs = {}
+        for name, fn in calls.items():
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                fn()
+            graphs[name] = gr
+        for gr in graphs.values():
+            gr.replay()
+        torch.cuda.synchronize()
+        for name, gr in graphs.items():
+            graph_us[name] = round(1e3 * _event_ms(gr.replay, 50), 1)
+        graph_us["step"] = round(sum(graph_us.values()), 1)
+    except Exception as exc:  # graph capture is an extra measurement only
+        print(f"[bench] graph timing skipped: {exc}", file=sys.stderr, flush=True)
+        graph_us = None
+    us_attn_kernel = graph_us["sparse_attention"] if graph_us else us_attn
+    # HBM bytes of the attention: K and V of every distinct visible page once per
+    # row and group, plus q and out.
+    pages = 0
+    for row in ids.cpu().view(-1, ids.shape[2]).tolist():
+        pages += len({p for p in row if p >= 0})
+    attn_bytes = pages * 64 * D * 2 * 2 + 2 * B * H * D * 2
+    gbs = attn_bytes / (us_attn_kernel * 1e-6) / 1e9
+    result = {
+        "metric": "decode step us/layer @128K context",
+        "value": graph_us["step"] if graph_us else round(us_step, 1),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round((graph_us["step"] if graph_us else us_step) / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": f"synthetic: {B} sequence(s) with {ctx} random N(0,1) bf16 keys/values in the cache, "
+                "random queries and new tokens; value = the step's three calls replayed from HIP "
+                "graphs (GPU time, no host launch overhead), eager_wall_us = the same step "
+                "called from Python",
+        "config": {"workload": args.workload, "batch": B, "context": ctx, "heads_q": H,
+                   "heads_kv": G, "head_dim": D, "page": 64, "budget_pages": topk,
+                   "sink_pages": init, "local_blocks": local, "selector": "stage-1 (decode)",
+                   "parallelism": "single-gpu"},
+        "eager_wall_us": round(us_step, 1),
+        "stages_us": graph_us or {"append_and_compress": round(us_append, 1),
+                                  "select": round(us_select, 1),
+                                  "sparse_attention": round(us_attn, 1)},
+        "stages_eager_us": {"append_and_compress": round(us_append, 1),
+                            "select": round(us_select, 1), "sparse_attention": round(us_attn, 1)},
+        "roofline": {"kernel": "ls_decode_attn_kernel + ls_decode_combine_kernel (split-K decode)",
+                     "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": attn_bytes},
+    }
+    if not args.no_cpu_baseline:
+        import oracle
+        threads = len(os.sched_getaffinity(0))
+        if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+            threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+        torch.set_num_threads(threads)
+        print(f"[bench] CPU baseline on {threads} threads ...", file=sys.stderr, flush=True)
+        qc = q[-1].cpu()
+        ncs = [n_windows(x) for x in lens]
+        kcp = torch.cat([kc[b, :ncs[b]].cpu() for b in range(B)])
+        kp = torch.cat([k[b, :lens[b]].cpu() for b in range(B)])
+        vp = torch.cat([v[b, :lens[b]].cpu() for b in range(B)])
+        cu_kc = [0]
+        cu_k = [0]
+        for b in range(B):
+            cu_kc.append(cu_kc[-1] + ncs[b])
+            cu_k.append(cu_k[-1] + lens[b])
+        def cpu_step():
+            ids_c = oracle.decode_select(qc, kcp, cu_q_host, cu_kc, lens, topk=topk,
+                                         init_blocks=init, local_blocks=local)
+            return oracle.sparse_attention(qc, kp, vp, cu_q_host, cu_k, ids_c, causal=False)
+        cpu_step()
+        t, n = _median_s(cpu_step, 3, 60.0)
+        result["cpu_baseline"] = {
+            "value": round(1e6 * t, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(),
+            "sample": (f"the oracle's decode step (stage-1 scores, page max-pool, top-k, then "
+                       f"float64 attention over the plan) for all {B} row(s) on the host CPU, "
+                       f"median of {n} warm runs"),
+        }
+    print(json.dumps(result), flush=True)
+
+
 def model_bench(args, dev) -> None:
     """Whole-model prefill: seconds per prefill plus one layer's stage breakdown."""
     import torch.nn.functional as F
@@ -404,6 +583,9 @@ def main() -> None:
     wl = WORKLOADS[args.workload]
     if wl.get("model"):
         model_bench(args, dev)
+        return
+    if wl.get("decode"):
+        decode_bench(args, dev)
         return
     print(f"[bench] generating {args.workload} ...", file=sys.stderr, flush=True)
     nosa = args.variant == "nosa"

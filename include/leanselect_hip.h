@@ -494,8 +494,9 @@ int ls_decode_select(const void* q, int64_t q_row_stride, const int32_t* cu_seql
  * topk], each page once) with j < cache_seqlens[b] (causal = 0) or
  * j <= cache_seqlens[b] - len_q(b) + i (causal = 1).  out [total_q, H, D] in
  * the cache dtype, softmax_lse float32 [H, total_q] (natural log; +inf and a
- * zero row when no key is visible) or NULL.  Split-K over n_splits slices of
- * each plan (1 <= n_splits <= topk), merged by a second kernel.  head_dim 128,
+ * zero row when no key is visible) or NULL.  Split-K: each (row, group) plan
+ * is cut into n_splits slices (1 <= n_splits <= 64), each run by a workgroup of
+ * four waves, and the slices are merged by a second kernel.  head_dim 128,
  * at most 16 query heads per KV head.  Workspace from
  * ls_sparse_attn_kvcache_workspace_size.
  * Replaces infllmv2_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=,

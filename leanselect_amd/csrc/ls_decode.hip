@@ -223,16 +223,24 @@ __global__ __launch_bounds__(256) void ls_stage1_finish_kernel(
   const int nc = cu_kc[b + 1] - cu_kc[b];
   const int nch = (nc + 63) / 64;
   const float* prow = part + ((int64_t)g * total_q + t) * n_chunks * 32;
-  if (tid < gs) {
+  {
+    // Sixteen consecutive threads per head (four heads per wave) reduce the
+    // head's chunk partials: each a strided share, then butterfly shuffles.
+    const int h = tid >> 4, part = tid & 15;
     float M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, prow[c * 32 + 2 * tid]);
+    if (h < gs)
+      for (int c = part; c < nch; c += 16) M = fmaxf(M, prow[c * 32 + 2 * h]);
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) M = fmaxf(M, ls_shfl_xor(M, o));
     float L = 0.f;
-    if (M != -INFINITY)
-      for (int c = 0; c < nch; ++c) {
-        const float mc = prow[c * 32 + 2 * tid];
-        if (mc != -INFINITY) L += prow[c * 32 + 2 * tid + 1] * __builtin_amdgcn_exp2f(mc - M);
+    if (h < gs && M != -INFINITY)
+      for (int c = part; c < nch; c += 16) {
+        const float mc = prow[c * 32 + 2 * h];
+        if (mc != -INFINITY) L += prow[c * 32 + 2 * h + 1] * __builtin_amdgcn_exp2f(mc - M);
       }
-    s_lse[tid] = M + __log2f(L);
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) L += ls_shfl_xor(L, o);
+    if (h < gs && part == 0) s_lse[h] = M + __log2f(L);
   }
   __syncthreads();
   const float* xrow = x + ((int64_t)g * total_q + t) * 16 * ncpad;
@@ -324,34 +332,46 @@ __global__ __launch_bounds__(256) void ls_decode_topk_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Split-K attention over the cache.  Workgroup (split s, row t, group g) is
-// one wave: it runs the pages of plan slots [s*pps, (s+1)*pps) of row t
-// (valid ids, each page once: a slot repeating an earlier slot's id is
-// skipped) with an online softmax and writes the split's per-head maximum,
-// sum and unnormalised O to the workspace; the combine kernel merges the
-// splits.  Keys visible to row t of sequence b (i = t - cu_q[b]):
-// j < len_b (causal=false) or j <= len_b - len_q(b) + i (causal, the
-// bottom-right alignment of flash-attention's kvcache call).
+// Split-K attention over the cache.  Workgroup (split s, row t, group g) has
+// four waves; wave w runs the pages of plan slots
+// [(4 s + w) ppw, (4 s + w + 1) ppw) of row t (valid ids, each page once: a
+// slot repeating an earlier slot's id is skipped) with an online softmax.  The
+// four waves merge their per-head maximum, sum and unnormalised O through LDS
+// and write one partial per workgroup; the combine kernel merges the splits.
+// Keys visible to row t of sequence b (i = t - cu_q[b]): j < len_b
+// (causal=false) or j <= len_b - len_q(b) + i (causal, the bottom-right
+// alignment of flash-attention's kvcache call).
 // S^T = K . Q^T (keys rows, heads columns) on the bf16/fp16 MFMA, with the
 // keys of each 32-key chunk permuted so lane group q holds keys 8q..8q+7 of
 // the chunk: P^T then feeds O^T = V^T . P^T from registers.  P is split into
 // a 16-bit head and a 16-bit remainder (two MFMAs) so it carries about 16
-// significant bits; V^T fragments come from an LDS copy of the page.
+// significant bits; V^T fragments come from the wave's LDS copy of the page.
 // ---------------------------------------------------------------------------
 #define LS_DEC_VPITCH 260  // bytes per staged V row (65 dwords: conflict-free transposed reads)
+#define LS_DEC_VBYTES (64 * LS_DEC_VPITCH)
+#define LS_DEC_PART (16 * 128 + 32)  // floats per partial: O [16][128], m [16], l [16]
+#define LS_DEC_MAX_SPLITS 64
+
+__device__ __forceinline__ void ls_dec_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 template <int DT>
-__global__ __launch_bounds__(64) void ls_decode_attn_kernel(
+__global__ __launch_bounds__(256) void ls_decode_attn_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, const int32_t* __restrict__ cu_q, int batch,
     int64_t total_q, const uint16_t* __restrict__ kc_, const uint16_t* __restrict__ vc_,
     int64_t cbs, int64_t crs, const int32_t* __restrict__ cache_seqlens, int gs, int D,
-    const int32_t* __restrict__ topk_idx, int topk, int pps, int n_splits, float scale_log2,
+    const int32_t* __restrict__ topk_idx, int topk, int ppw, int n_splits, float scale_log2,
     int causal, float* __restrict__ part) {
   const int s = LS_BID_X;
   const int64_t t = LS_BID_Y;
   const int g = LS_BID_Z;
-  const int lane = LS_TID, r = lane & 15, qg = lane >> 4;
-  __shared__ __attribute__((aligned(16))) uint8_t s_v[64 * LS_DEC_VPITCH];
+  const int tid = LS_TID, lane = tid & 63, w = tid >> 6;
+  const int r = lane & 15, qg = lane >> 4;
+  __shared__ __attribute__((aligned(16))) uint8_t s_v[4][LS_DEC_VBYTES];
+  uint8_t* sv_w = s_v[w];
   const int b = ls_find_segment(cu_q, batch, t);
   const int64_t len_b = cache_seqlens[b];
   const int64_t i_row = t - cu_q[b];
@@ -371,7 +391,7 @@ __global__ __launch_bounds__(64) void ls_decode_attn_kernel(
   const int32_t* idrow = topk_idx + ((int64_t)g * total_q + t) * topk;
   const uint16_t* kseq = kc_ + (int64_t)b * cbs + (int64_t)g * D;
   const uint16_t* vseq = vc_ + (int64_t)b * cbs + (int64_t)g * D;
-  const int slot0 = s * pps, slot1 = min(topk, slot0 + pps);
+  const int slot0 = (4 * s + w) * ppw, slot1 = min(topk, slot0 + ppw);
   for (int slot = slot0; slot < slot1; ++slot) {
     const int id = idrow[slot];
     if (id < 0 || (int64_t)id >= n_pages || 64LL * id >= limit) continue;
@@ -384,13 +404,13 @@ __global__ __launch_bounds__(64) void ls_decode_attn_kernel(
     if (dup) continue;
     const int64_t key0 = 64LL * id;
     const int64_t nvis = min((int64_t)64, limit - key0);  // visible keys of this page (> 0)
-    // Stage V (keys past nvis as zeros) into LDS, rows of 128 values.
+    // Stage V (keys past nvis as zeros) into the wave's LDS, rows of 128 values.
 #pragma unroll
     for (int it = 0; it < 16; ++it) {
       const int ci = it * 64 + lane, kr = ci >> 4, c16 = ci & 15;
       ls_u32x4 v = {0u, 0u, 0u, 0u};
       if (kr < nvis) v = ls_load16(vseq + (key0 + kr) * crs + 8 * c16);
-      uint32_t* dst = reinterpret_cast<uint32_t*>(s_v + kr * LS_DEC_VPITCH + 16 * c16);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(sv_w + kr * LS_DEC_VPITCH + 16 * c16);
       dst[0] = v[0];
       dst[1] = v[1];
       dst[2] = v[2];
@@ -427,7 +447,7 @@ __global__ __launch_bounds__(64) void ls_decode_attn_kernel(
     l_run *= alpha;
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[db] *= alpha;
-    __syncthreads();  // the page's V rows are in LDS
+    ls_dec_wave_sync();  // the page's V rows are in the wave's LDS
 #pragma unroll
     for (int cch = 0; cch < 2; ++cch) {
       // P^T fragment: lane (r, qg) holds head r, keys 32 cch + 8 qg + 0..7
@@ -450,7 +470,7 @@ __global__ __launch_bounds__(64) void ls_decode_attn_kernel(
 #pragma unroll
       for (int db = 0; db < 8; ++db) {
         // V^T fragment: lane (r, qg) holds dim 16 db + r of keys 32 cch + 8 qg + 0..7.
-        const uint8_t* vp = s_v + (32 * cch + 8 * qg) * LS_DEC_VPITCH + 2 * (16 * db + r);
+        const uint8_t* vp = sv_w + (32 * cch + 8 * qg) * LS_DEC_VPITCH + 2 * (16 * db + r);
         uint16_t e[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) e[k] = *reinterpret_cast<const uint16_t*>(vp + k * LS_DEC_VPITCH);
@@ -460,23 +480,50 @@ __global__ __launch_bounds__(64) void ls_decode_attn_kernel(
         o[db] = LsElem<DT>::mfma(vf, plo, o[db]);
       }
     }
-    __syncthreads();  // all reads of s_v done before the next page overwrites it
+    ls_dec_wave_sync();  // all reads of the page's V done before the next page overwrites it
   }
   l_run += ls_shfl_xor(l_run, 16);
   l_run += ls_shfl_xor(l_run, 32);
-  // Partial of this split: [16 heads][128 dims] O, then m[16], l[16].
-  float* pp = part + (((int64_t)g * total_q + t) * n_splits + s) * (16 * 128 + 32);
+  // The wave's state into its LDS block: O [16][128], then m [16], l [16].
+  float* st = reinterpret_cast<float*>(sv_w);
 #pragma unroll
   for (int db = 0; db < 8; ++db)  // o[db][i]: head r, dim 16 db + 4 qg + i
-    *reinterpret_cast<ls_f32x4*>(pp + r * 128 + 16 * db + 4 * qg) = o[db];
+    *reinterpret_cast<ls_f32x4*>(st + r * 128 + 16 * db + 4 * qg) = o[db];
   if (qg == 0) {
-    pp[16 * 128 + r] = m_run;
-    pp[16 * 128 + 16 + r] = l_run;
+    st[16 * 128 + r] = m_run;
+    st[16 * 128 + 16 + r] = l_run;
+  }
+  __syncthreads();
+  // Merge the four waves: thread e-range of the 16 x 128 outputs.
+  float* pp = part + (((int64_t)g * total_q + t) * n_splits + s) * LS_DEC_PART;
+  for (int e = tid; e < 16 * 128; e += 256) {
+    const int h = e >> 7, d = e & 127;
+    float mw[4], M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mw[i] = reinterpret_cast<const float*>(s_v[i])[16 * 128 + h];
+      M = fmaxf(M, mw[i]);
+    }
+    float acc = 0.f, L = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (mw[i] == -INFINITY) continue;
+      const float wt = __builtin_amdgcn_exp2f(mw[i] - M);
+      const float* si = reinterpret_cast<const float*>(s_v[i]);
+      acc += wt * si[h * 128 + d];
+      L += wt * si[16 * 128 + 16 + h];
+    }
+    pp[h * 128 + d] = acc;
+    if (d == 0) {
+      pp[16 * 128 + h] = M;
+      pp[16 * 128 + 16 + h] = L;
+    }
   }
 }
 
 // out[t][g*gs + h][:] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s; rows
-// without a visible key give zeros and lse = +inf.
+// without a visible key give zeros and lse = +inf.  The splits' weights are
+// formed once per head in LDS; each output is then a sum of independent loads.
 template <int DT>
 __global__ __launch_bounds__(256) void ls_decode_combine_kernel(
     const float* __restrict__ part, int64_t total_q, int gs, int D, int n_splits,
@@ -485,27 +532,37 @@ __global__ __launch_bounds__(256) void ls_decode_combine_kernel(
   const int g = LS_BID_Y;
   const int tid = LS_TID;
   const int G = gridDim.y;
-  const float* pr = part + ((int64_t)g * total_q + t) * n_splits * (16 * 128 + 32);
-  for (int e = tid; e < gs * 128; e += 256) {
-    const int h = e >> 7, d = e & 127;
+  __shared__ float s_w[LS_DEC_MAX_SPLITS][16];
+  __shared__ float s_m[LS_DEC_MAX_SPLITS][16];
+  __shared__ float s_l[LS_DEC_MAX_SPLITS][16];
+  __shared__ float s_lse[16];
+  const float* pr = part + ((int64_t)g * total_q + t) * n_splits * LS_DEC_PART;
+  for (int i = tid; i < n_splits * 16; i += 256) {
+    const int sp = i >> 4, h = i & 15;
+    s_m[sp][h] = pr[sp * LS_DEC_PART + 16 * 128 + h];
+    s_l[sp][h] = pr[sp * LS_DEC_PART + 16 * 128 + 16 + h];
+  }
+  __syncthreads();
+  if (tid < 16) {
     float M = -INFINITY;
-    for (int s = 0; s < n_splits; ++s) M = fmaxf(M, pr[s * (16 * 128 + 32) + 16 * 128 + h]);
-    float L = 0.f, acc = 0.f;
-    if (M != -INFINITY) {
-      for (int s = 0; s < n_splits; ++s) {
-        const float* ps = pr + s * (16 * 128 + 32);
-        const float ms = ps[16 * 128 + h];
-        if (ms == -INFINITY) continue;
-        const float w = __builtin_amdgcn_exp2f(ms - M);
-        L += w * ps[16 * 128 + 16 + h];
-        acc += w * ps[h * 128 + d];
-      }
+    for (int sp = 0; sp < n_splits; ++sp) M = fmaxf(M, s_m[sp][tid]);
+    float L = 0.f;
+    for (int sp = 0; sp < n_splits; ++sp) {
+      const float wt = s_m[sp][tid] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[sp][tid] - M);
+      s_w[sp][tid] = wt;
+      L += wt * s_l[sp][tid];
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    out[(t * G + g) * (int64_t)gs * D + (int64_t)h * D + d] = LsElem<DT>::from_f(acc * inv);
-    if (lse && d == 0)
-      lse[((int64_t)g * gs + h) * total_q + t] =
-          L > 0.f ? (M + __log2f(L)) * 0.69314718055994531f : INFINITY;
+    for (int sp = 0; sp < n_splits; ++sp) s_w[sp][tid] *= inv;
+    s_lse[tid] = L > 0.f ? (M + __log2f(L)) * 0.69314718055994531f : INFINITY;
+  }
+  __syncthreads();
+  for (int e = tid; e < gs * 128; e += 256) {
+    const int h = e >> 7, d = e & 127;
+    float acc = 0.f;
+    for (int sp = 0; sp < n_splits; ++sp) acc += s_w[sp][h] * pr[sp * LS_DEC_PART + h * 128 + d];
+    out[(t * G + g) * (int64_t)gs * D + (int64_t)h * D + d] = LsElem<DT>::from_f(acc);
+    if (lse && d == 0) lse[((int64_t)g * gs + h) * total_q + t] = s_lse[h];
   }
 }
 
@@ -699,7 +756,7 @@ extern "C" int ls_decode_select(const void* q, int64_t q_row_stride, const int32
 extern "C" size_t ls_sparse_attn_kvcache_workspace_size(int64_t total_q, int32_t num_kv_heads,
                                                         int32_t n_splits) {
   return ls_align256(4 * (size_t)total_q * num_kv_heads * (n_splits > 0 ? n_splits : 1) *
-                     (16 * 128 + 32));
+                     LS_DEC_PART);
 }
 
 extern "C" int ls_sparse_attn_kvcache(const void* q, int64_t q_row_stride,
@@ -719,8 +776,8 @@ extern "C" int ls_sparse_attn_kvcache(const void* q, int64_t q_row_stride,
              "ls_sparse_attn_kvcache: head_dim 128 and at most 16 query heads per KV head");
   LS_REQUIRE(dtype == LS_BF16 || dtype == LS_F16, LS_ERR_UNSUPPORTED,
              "ls_sparse_attn_kvcache: bf16 or fp16");
-  LS_REQUIRE(topk >= 1 && n_splits >= 1 && n_splits <= topk, LS_ERR_INVALID,
-             "ls_sparse_attn_kvcache: need topk >= 1 and 1 <= n_splits <= topk");
+  LS_REQUIRE(topk >= 1 && n_splits >= 1 && n_splits <= LS_DEC_MAX_SPLITS, LS_ERR_INVALID,
+             "ls_sparse_attn_kvcache: need topk >= 1 and 1 <= n_splits <= %d", LS_DEC_MAX_SPLITS);
   LS_REQUIRE(total_q <= 0x7fffffffLL && num_kv_heads <= 65535, LS_ERR_INVALID,
              "ls_sparse_attn_kvcache: too many rows or heads");
   LS_REQUIRE(q_row_stride % 8 == 0 && cache_row_stride % 8 == 0 && cache_batch_stride % 8 == 0,
@@ -733,28 +790,29 @@ extern "C" int ls_sparse_attn_kvcache(const void* q, int64_t q_row_stride,
   const size_t need = ls_sparse_attn_kvcache_workspace_size(total_q, num_kv_heads, n_splits);
   LS_REQUIRE(ws_bytes >= need, LS_ERR_WORKSPACE, "ls_sparse_attn_kvcache: workspace %zu < %zu",
              ws_bytes, need);
-  const int pps = (topk + n_splits - 1) / n_splits;
-  const int splits = (topk + pps - 1) / pps;
+  // Four waves per split, ppw plan slots per wave.
+  const int ppw = (topk + 4 * n_splits - 1) / (4 * n_splits);
+  const int splits = (topk + 4 * ppw - 1) / (4 * ppw);
   hipStream_t s = (hipStream_t)stream;
   const float scale_log2 = softmax_scale * 1.4426950408889634f;
   float* part = (float*)ws;
   const dim3 grid((unsigned)splits, (unsigned)total_q, num_kv_heads);
   const dim3 cgrid((unsigned)total_q, num_kv_heads);
   if (dtype == LS_BF16) {
-    hipLaunchKernelGGL(ls_decode_attn_kernel<LS_BF16>, grid, dim3(64), 0, s, (const uint16_t*)q,
+    hipLaunchKernelGGL(ls_decode_attn_kernel<LS_BF16>, grid, dim3(256), 0, s, (const uint16_t*)q,
                        q_row_stride, cu_seqlens_q, batch, total_q, (const uint16_t*)k_cache,
                        (const uint16_t*)v_cache, cache_batch_stride, cache_row_stride,
-                       cache_seqlens, gs, head_dim, topk_idx, topk, pps, splits, scale_log2,
+                       cache_seqlens, gs, head_dim, topk_idx, topk, ppw, splits, scale_log2,
                        causal, part);
     int rc = ls_check_launch("ls_decode_attn_kernel");
     if (rc) return rc;
     hipLaunchKernelGGL(ls_decode_combine_kernel<LS_BF16>, cgrid, dim3(256), 0, s, part, total_q,
                        gs, head_dim, splits, (uint16_t*)out, softmax_lse);
   } else {
-    hipLaunchKernelGGL(ls_decode_attn_kernel<LS_F16>, grid, dim3(64), 0, s, (const uint16_t*)q,
+    hipLaunchKernelGGL(ls_decode_attn_kernel<LS_F16>, grid, dim3(256), 0, s, (const uint16_t*)q,
                        q_row_stride, cu_seqlens_q, batch, total_q, (const uint16_t*)k_cache,
                        (const uint16_t*)v_cache, cache_batch_stride, cache_row_stride,
-                       cache_seqlens, gs, head_dim, topk_idx, topk, pps, splits, scale_log2,
+                       cache_seqlens, gs, head_dim, topk_idx, topk, ppw, splits, scale_log2,
                        causal, part);
     int rc = ls_check_launch("ls_decode_attn_kernel");
     if (rc) return rc;

@@ -188,9 +188,10 @@ def sparse_attention_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
     q = q if (q.stride(2) == 1 and q.stride(1) == D) else q.contiguous()
     K = topk_idx.shape[2]
     if n_splits is None:
-        # Enough waves to cover the device when there are few rows.
-        n_splits = max(1, min(K, -(-512 // max(1, total_q * G))))
-    n_splits = max(1, min(int(n_splits), K))
+        # Workgroups of four waves per (row, group): enough of them to cover the
+        # device when there are few rows, at least one page per wave.
+        n_splits = max(1, min(-(-K // 4), -(-256 // max(1, total_q * G))))
+    n_splits = max(1, min(int(n_splits), 64))
     if out is None:
         out = torch.empty((total_q, H, D), dtype=q.dtype, device=dev)
     lse = torch.empty((H, total_q), dtype=torch.float32, device=dev) if return_lse else None
