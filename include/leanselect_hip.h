@@ -469,7 +469,7 @@ int ls_kvcache_append(void* k_cache, void* v_cache, int64_t cache_batch_stride,
  * (ties to the lower page), ascending, ids past the row's own page replaced
  * by -1.  topk_idx: int32 [G, total_q, take].  max_kc = n_c of the longest
  * sequence; out_len = ceil((max len_q + max(len - len_q)) / block_size)
- * (< 65536).  head_dim 128, at most 16 query heads per KV head; kc_cache rows
+ * (at most 32768).  head_dim 128, at most 16 query heads per KV head; kc_cache rows
  * dense (kc_row_stride = G * D).  Workspace from
  * ls_decode_select_workspace_size.
  * Replaces compressed_attention with cache_lens (leanselect/models/minicpm.py:594-705,
@@ -497,7 +497,7 @@ int ls_decode_select(const void* q, int64_t q_row_stride, const int32_t* cu_seql
  * zero row when no key is visible) or NULL.  Split-K: each (row, group) plan
  * is cut into n_splits slices (1 <= n_splits <= 64), each run by a workgroup of
  * four waves, and the slices are merged by a second kernel.  head_dim 128,
- * at most 16 query heads per KV head.  Workspace from
+ * at most 16 query heads per KV head, topk <= 256.  Workspace from
  * ls_sparse_attn_kvcache_workspace_size.
  * Replaces infllmv2_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=,
  * causal=, topk_idx=) (third_party/infllmv2/paper1.patch:2511-2615) and the

@@ -87,7 +87,10 @@ __global__ __launch_bounds__(256) void ls_cache_compress_kernel(
   const int b = ls_find_segment(cu_win, batch, wi);
   const int64_t w = ls_n_windows(cache_seqlens[b], ks, stride) + (wi - cu_win[b]);
   const uint16_t* src = kcache + (int64_t)b * cbs + (w * stride) * crs + (int64_t)g * D + 8 * c;
+  // Unrolled so that a block of row loads is in flight at once; the sums
+  // still run in token order.
   auto add_rows = [&](int r0, int r1, float (&s)[8]) {
+#pragma unroll 16
     for (int t = r0; t < r1; ++t) {
       const ls_u32x4 a = ls_load16(src + (int64_t)t * crs);
 #pragma unroll
@@ -117,32 +120,22 @@ __global__ __launch_bounds__(256) void ls_cache_compress_kernel(
 
 // ---------------------------------------------------------------------------
 // Stage-1 decode scores.  Row t (sequence b) and KV group g:
-//   score[g][t][j] = sum_{h in g} softmax_j(scale * q[t][h] . kc[b][j][g])
+//   score[j] = sum_{h in g} softmax_j(scale * q[t][h] . kc[b][j][g])
 // over the n_c(b) compressed keys of the sequence (no causal limit: the
 // reference calls stage 1 with causal=False when decoding), rounded to the
-// query dtype and then to bf16 (compressed_attention's .to(bfloat16)).
-// Columns n_c(b) <= j < max_kc are written as 0.
+// query dtype and then to bf16 (compressed_attention's .to(bfloat16)), then
+// max-pooled into pages.  n_c(b) is the window count of the sequence's
+// current length, clipped to max_kc.
 //
 // Pass 1 (one wave per 64-key chunk, row and group): S^T = Kc . Q^T on the
 // 16x16x32 MFMA (keys are rows, the group's heads columns); the raw scores in
 // base-2 units go to the workspace with each head's chunk maximum and
-// sum of 2^(x - max).  Pass 2 (one workgroup per row and group): each head's
-// log2-sum-exp from the chunk partials, then the group sums per key.
+// sum of 2^(x - max).  Pass 2 (one workgroup per block of pages, row and
+// group): each head's log2-sum-exp from the chunk partials, the scores of the
+// keys in the block's page windows, and their page maxima.
 // ---------------------------------------------------------------------------
-// cu_kc[b] = sum_{b' < b} n_c(b') over the sequences' current lengths;
-// cache_lens[b] = len_b - len_q(b), the tokens before the sequence's rows.
-__global__ void ls_decode_plan_kernel(const int32_t* __restrict__ cache_seqlens,
-                                      const int32_t* __restrict__ cu_q, int batch, int ks,
-                                      int stride, int32_t* __restrict__ cu_kc,
-                                      int32_t* __restrict__ cache_lens) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int32_t acc = 0;
-  cu_kc[0] = 0;
-  for (int b = 0; b < batch; ++b) {
-    acc += (int32_t)ls_n_windows(cache_seqlens[b], ks, stride);
-    cu_kc[b + 1] = acc;
-    cache_lens[b] = cache_seqlens[b] - (cu_q[b + 1] - cu_q[b]);
-  }
+__device__ __forceinline__ int ls_dec_n_c(int64_t len, int ks, int stride, int64_t max_kc) {
+  return (int)min(ls_n_windows(len, ks, stride), max_kc);
 }
 
 // x[g][t][h][j] (float, base-2 units, -inf past n_c), part[g][t][c][h] = (max, sum).
@@ -150,14 +143,15 @@ template <int DT>
 __global__ __launch_bounds__(64) void ls_stage1_chunk_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, const int32_t* __restrict__ cu_q, int batch,
     int64_t total_q, const uint16_t* __restrict__ kcc, int64_t kbs, int64_t krs,
-    const int32_t* __restrict__ cu_kc, int gs, int D, float scale_log2, int64_t ncpad,
-    int n_chunks, float* __restrict__ x, float* __restrict__ part) {
+    const int32_t* __restrict__ cache_seqlens, int ks, int stride, int64_t max_kc, int gs, int D,
+    float scale_log2, int64_t ncpad, int n_chunks, float* __restrict__ x,
+    float* __restrict__ part) {
   const int c = LS_BID_X;
   const int64_t t = LS_BID_Y;
   const int g = LS_BID_Z;
   const int lane = LS_TID, r = lane & 15, qg = lane >> 4;
   const int b = ls_find_segment(cu_q, batch, t);
-  const int nc = cu_kc[b + 1] - cu_kc[b];
+  const int nc = ls_dec_n_c(cache_seqlens[b], ks, stride, max_kc);
   float* xrow = x + ((int64_t)g * total_q + t) * 16 * ncpad;
   float* prow = part + (((int64_t)g * total_q + t) * n_chunks + c) * 32;
   // Q^T fragments (B operand): lane (r, qg) holds head r, dims 32 ks + 8 qg + 0..7.
@@ -165,8 +159,8 @@ __global__ __launch_bounds__(64) void ls_stage1_chunk_kernel(
   const bool head_ok = r < gs;
   const uint16_t* qrow = q + t * qrs + ((int64_t)g * gs + r) * D + 8 * qg;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-    qf[ks] = head_ok ? ls_load16(qrow + 32 * ks) : ls_u32x4{0u, 0u, 0u, 0u};
+  for (int k4 = 0; k4 < 4; ++k4)
+    qf[k4] = head_ok ? ls_load16(qrow + 32 * k4) : ls_u32x4{0u, 0u, 0u, 0u};
   float m = -INFINITY;
   float sv[16];
 #pragma unroll
@@ -176,9 +170,9 @@ __global__ __launch_bounds__(64) void ls_stage1_chunk_kernel(
     const bool key_ok = j < nc;
     const uint16_t* krow = kcc + (int64_t)b * kbs + (int64_t)j * krs + (int64_t)g * D + 8 * qg;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const ls_u32x4 kf = key_ok ? ls_load16(krow + 32 * ks) : ls_u32x4{0u, 0u, 0u, 0u};
-      acc = LsElem<DT>::mfma(kf, qf[ks], acc);
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const ls_u32x4 kf = key_ok ? ls_load16(krow + 32 * k4) : ls_u32x4{0u, 0u, 0u, 0u};
+      acc = LsElem<DT>::mfma(kf, qf[k4], acc);
     }
     // acc[i]: head r (column), key 64 c + 16 kb + 4 qg + i (row).
 #pragma unroll
@@ -210,127 +204,199 @@ __global__ __launch_bounds__(64) void ls_stage1_chunk_kernel(
   }
 }
 
+// Pass 2 and the page max-pool of max_pooling_1d_varlen, fused.  Workgroup
+// (page block pb, row t, group g) covers pages [ppb pb, ppb pb + ppb) of
+// sp = block_size / kernel_stride keys each (ppb sp <= 256).  It forms each
+// head's log2-sum-exp from the chunk partials, scores the keys
+// [ppb sp pb - 1, ppb sp (pb + 1)) into LDS (-inf outside [0, n_c)), and writes
+//   pooled[g][t][p] = +inf            if p < init_blocks or
+//                                        q_page - local_blocks <= p <= q_page,
+//                     max of the scores of keys [p sp - 1, p sp + sp)  otherwise
+// (-inf when none exists), q_page = (len_b - len_q(b) + i) / block_size for
+// row i of sequence b.
 template <int DT>
-__global__ __launch_bounds__(256) void ls_stage1_finish_kernel(
+__global__ __launch_bounds__(256) void ls_stage1_pool_kernel(
     const float* __restrict__ x, const float* __restrict__ part, const int32_t* __restrict__ cu_q,
-    int batch, int64_t total_q, const int32_t* __restrict__ cu_kc, int gs, int64_t ncpad,
-    int n_chunks, int64_t max_kc, uint16_t* __restrict__ score) {
-  const int64_t t = LS_BID_X;
-  const int g = LS_BID_Y;
+    int batch, int64_t total_q, const int32_t* __restrict__ cache_seqlens, int ks, int stride,
+    int64_t max_kc, int gs, int64_t ncpad, int n_chunks, int sp, int ppb, int64_t out_len,
+    int block_size, int init_blocks, int local_blocks, uint16_t* __restrict__ pooled) {
+  const int64_t p0 = (int64_t)ppb * LS_BID_X;
+  const int64_t t = LS_BID_Y;
+  const int g = LS_BID_Z;
   const int tid = LS_TID;
   __shared__ float s_lse[16];
+  __shared__ float s_sc[257];
   const int b = ls_find_segment(cu_q, batch, t);
-  const int nc = cu_kc[b + 1] - cu_kc[b];
-  const int nch = (nc + 63) / 64;
-  const float* prow = part + ((int64_t)g * total_q + t) * n_chunks * 32;
-  {
+  const int64_t len_b = cache_seqlens[b];
+  const int nc = ls_dec_n_c(len_b, ks, stride, max_kc);
+  const int64_t j0 = p0 * sp - 1;  // key of LDS slot 0
+  const int n_keys = ppb * sp + 1;
+  const bool has_keys = max((int64_t)0, j0) < (int64_t)nc;  // uniform
+  if (has_keys) {
     // Sixteen consecutive threads per head (four heads per wave) reduce the
     // head's chunk partials: each a strided share, then butterfly shuffles.
-    const int h = tid >> 4, part = tid & 15;
+    const float* prow = part + ((int64_t)g * total_q + t) * n_chunks * 32;
+    const int nch = (nc + 63) / 64;
+    const int h = tid >> 4, share = tid & 15;
     float M = -INFINITY;
     if (h < gs)
-      for (int c = part; c < nch; c += 16) M = fmaxf(M, prow[c * 32 + 2 * h]);
+      for (int c = share; c < nch; c += 16) M = fmaxf(M, prow[c * 32 + 2 * h]);
 #pragma unroll
     for (int o = 8; o >= 1; o >>= 1) M = fmaxf(M, ls_shfl_xor(M, o));
     float L = 0.f;
     if (h < gs && M != -INFINITY)
-      for (int c = part; c < nch; c += 16) {
+      for (int c = share; c < nch; c += 16) {
         const float mc = prow[c * 32 + 2 * h];
         if (mc != -INFINITY) L += prow[c * 32 + 2 * h + 1] * __builtin_amdgcn_exp2f(mc - M);
       }
 #pragma unroll
     for (int o = 8; o >= 1; o >>= 1) L += ls_shfl_xor(L, o);
-    if (h < gs && part == 0) s_lse[h] = M + __log2f(L);
+    if (h < gs && share == 0) s_lse[h] = M + __log2f(L);
   }
   __syncthreads();
   const float* xrow = x + ((int64_t)g * total_q + t) * 16 * ncpad;
-  uint16_t* orow = score + ((int64_t)g * total_q + t) * max_kc;
-  for (int64_t j = tid; j < max_kc; j += 256) {
-    uint16_t o = 0;
-    if (j < nc) {
+  for (int i = tid; i < n_keys; i += 256) {
+    const int64_t j = j0 + i;
+    float v = -INFINITY;
+    if (j >= 0 && j < nc) {
       float s = 0.f;
       for (int h = 0; h < gs; ++h) s += __builtin_amdgcn_exp2f(xrow[(int64_t)h * ncpad + j] - s_lse[h]);
+      uint16_t o;
       if constexpr (DT == LS_F16)
         o = ls_f32_to_bf16(ls_f16_to_f32(ls_f32_to_f16(s)));
       else
         o = ls_f32_to_bf16(s);
+      v = ls_bf16_to_f32(o);
     }
-    orow[j] = o;
+    s_sc[i] = v;
+  }
+  __syncthreads();
+  const int64_t q_page = (len_b - (cu_q[b + 1] - cu_q[b]) + (t - cu_q[b])) / block_size;
+  uint16_t* orow = pooled + ((int64_t)g * total_q + t) * out_len;
+  for (int i = tid; i < ppb; i += 256) {
+    const int64_t p = p0 + i;
+    if (p >= out_len) break;
+    float v;
+    if (p < init_blocks || (q_page - local_blocks <= p && p <= q_page)) {
+      v = INFINITY;
+    } else {
+      v = -INFINITY;
+      for (int e = 0; e <= sp; ++e) v = fmaxf(v, s_sc[i * sp + e]);
+    }
+    orow[p] = ls_f32_to_bf16(v);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Decode top-k over pooled page scores pooled[g][t][out_len] (bf16, forced
-// pages +inf, pages past the row's own -inf): the `take` best pages (ties to
-// the lower page), ascending, ids past the row's page q_idx replaced by -1
-// (they sort last, so the list is the kept ids then -1 padding).  One
-// workgroup per (row, group); keys (value << 16 | (65535 - page)) are unique
-// and their take-th largest is found by an 8-bit radix select in four passes.
+// pages +inf, pages without keys -inf): the `take` best pages (ties to the
+// lower page), ascending, ids past the row's page q_idx replaced by -1 (they
+// sort last, so the list is the kept ids then -1 padding).  One workgroup per
+// (row, group).  The row's 16-bit order keys are held in LDS; the take-th
+// largest key T is found by a two-pass 8-bit radix select (histogram of the
+// high byte, then of the low byte among keys with T's high byte, each bucket
+// found with a parallel suffix sum), and the pages with key > T plus the
+// lowest-page m = take - #{key > T} pages with key == T are compacted in page
+// order (thread i owns a contiguous run of pages).
 // ---------------------------------------------------------------------------
+#define LS_DEC_TOPK_MAX_PAGES 32768  // LDS keys (64 KB)
+
 __global__ __launch_bounds__(256) void ls_decode_topk_kernel(
     const uint16_t* __restrict__ pooled, const int32_t* __restrict__ cu_q, int batch,
-    int64_t total_q, const int32_t* __restrict__ cache_lens, int out_len, int block_size,
+    int64_t total_q, const int32_t* __restrict__ cache_seqlens, int out_len, int block_size,
     int take, int32_t* __restrict__ ids) {
   const int64_t t = LS_BID_X;
   const int g = LS_BID_Y;
-  const int tid = LS_TID;
+  const int tid = LS_TID, lane = tid & 63, w = tid >> 6;
+  extern __shared__ uint16_t s_key[];  // out_len order keys
   __shared__ uint32_t s_hist[256];
-  __shared__ uint32_t s_sel[2];  // prefix found so far, keys still needed above it
-  __shared__ int32_t s_cnt[256];
+  __shared__ int32_t s_wtot[4];
+  __shared__ uint32_t s_sel[3];  // bucket, keys still needed inside it, keys above it
   const uint16_t* row = pooled + ((int64_t)g * total_q + t) * out_len;
   const int b = ls_find_segment(cu_q, batch, t);
-  const int64_t q_idx = ((int64_t)cache_lens[b] + (t - cu_q[b])) / block_size;
-  auto key_of = [&](int p) -> uint32_t {
-    return (ls_order_key16(row[p]) << 16) | (uint32_t)(65535 - p);
-  };
-  if (tid == 0) {
-    s_sel[0] = 0u;
-    s_sel[1] = (uint32_t)take;
-  }
-  for (int pass = 3; pass >= 0; --pass) {
-    s_hist[tid] = 0u;
-    __syncthreads();
-    const uint32_t prefix = s_sel[0];
-    const uint32_t hi_mask = pass == 3 ? 0u : (0xffffffffu << (8 * (pass + 1)));
-    for (int p = tid; p < out_len; p += 256) {
-      const uint32_t k = key_of(p);
-      if ((k & hi_mask) == (prefix & hi_mask)) atomicAdd(&s_hist[(k >> (8 * pass)) & 255u], 1u);
-    }
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t need = s_sel[1], acc = 0u;
-      int d = 255;
-      for (; d > 0; --d) {
-        if (acc + s_hist[d] >= need) break;
-        acc += s_hist[d];
-      }
-      s_sel[0] = prefix | ((uint32_t)d << (8 * pass));
-      s_sel[1] = need - acc;
-    }
-    __syncthreads();
-  }
-  const uint32_t T = s_sel[0];  // the take-th largest key
-  // Ordered compaction of the kept pages (key >= T, page <= q_idx).
-  const int per = (out_len + 255) / 256;
-  const int p0 = tid * per, p1 = min(out_len, p0 + per);
-  int cnt = 0;
-  for (int p = p0; p < p1; ++p) cnt += (key_of(p) >= T && p <= q_idx) ? 1 : 0;
-  s_cnt[tid] = cnt;
+  const int64_t q_idx =
+      ((int64_t)cache_seqlens[b] - (cu_q[b + 1] - cu_q[b]) + (t - cu_q[b])) / block_size;
+  for (int p = tid; p < out_len; p += 256) s_key[p] = (uint16_t)ls_order_key16(row[p]);
+  s_hist[tid] = 0u;
   __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {  // inclusive scan
-    const int v = tid >= off ? s_cnt[tid - off] : 0;
+  // The bucket d holding the need-th largest key: #{bucket > d} < need <= #{bucket >= d}.
+  auto find_bucket = [&](uint32_t need) {
+    const uint32_t h = s_hist[tid];
+    uint32_t sfx = h;  // keys in buckets tid .. (wave's last)
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t y = (uint32_t)__shfl_down((int)sfx, off, 64);
+      if (lane + off < 64) sfx += y;
+    }
+    if (lane == 0) s_wtot[w] = (int32_t)sfx;
     __syncthreads();
-    s_cnt[tid] += v;
+    for (int v = w + 1; v < 4; ++v) sfx += (uint32_t)s_wtot[v];
+    const uint32_t above = sfx - h;
+    if (h > 0u && sfx >= need && above < need) {
+      s_sel[0] = (uint32_t)tid;
+      s_sel[1] = need - above;
+      s_sel[2] = above;
+    }
     __syncthreads();
+  };
+  for (int p = tid; p < out_len; p += 256) atomicAdd(&s_hist[s_key[p] >> 8], 1u);
+  __syncthreads();
+  find_bucket((uint32_t)take);
+  const uint32_t hi = s_sel[0], need_lo = s_sel[1];
+  s_hist[tid] = 0u;
+  __syncthreads();
+  for (int p = tid; p < out_len; p += 256) {
+    const uint32_t k = s_key[p];
+    if ((k >> 8) == hi) atomicAdd(&s_hist[k & 255u], 1u);
   }
-  int pos = s_cnt[tid] - cnt;
-  const int kept = s_cnt[255];
+  __syncthreads();
+  find_bucket(need_lo);
+  const uint32_t T = (hi << 8) | s_sel[0];
+  const int m = (int)s_sel[1];  // keys equal to T that are taken (the lowest pages)
+  // Block-wide exclusive scan of one count per thread (also returns the total).
+  auto block_scan = [&](int v, int* total) {
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    __syncthreads();  // earlier readers of s_wtot are done
+    if (lane == 63) s_wtot[w] = x;
+    __syncthreads();
+    int before = x - v, tot = 0;
+    for (int v2 = 0; v2 < 4; ++v2) {
+      if (v2 < w) before += s_wtot[v2];
+      tot += s_wtot[v2];
+    }
+    *total = tot;
+    return before;
+  };
+  const int per = (out_len + 255) / 256;
+  const int p0 = min(out_len, tid * per), p1 = min(out_len, p0 + per);
+  int n_eq = 0;
+  for (int p = p0; p < p1; ++p) n_eq += s_key[p] == T ? 1 : 0;
+  int unused;
+  int eq_rank = block_scan(n_eq, &unused);
+  int n_keep = 0;
+  for (int p = p0; p < p1; ++p) {
+    const uint32_t k = s_key[p];
+    const bool sel = k > T || (k == T && eq_rank < m);
+    eq_rank += k == T ? 1 : 0;
+    n_keep += (sel && p <= q_idx) ? 1 : 0;
+  }
+  int kept;
+  int pos = block_scan(n_keep, &kept);
   int32_t* orow = ids + ((int64_t)g * total_q + t) * take;
-  for (int p = p0; p < p1; ++p)
-    if (key_of(p) >= T && p <= q_idx) orow[pos++] = p;
+  eq_rank = eq_rank - n_eq;  // back to this thread's first page
+  for (int p = p0; p < p1; ++p) {
+    const uint32_t k = s_key[p];
+    const bool sel = k > T || (k == T && eq_rank < m);
+    eq_rank += k == T ? 1 : 0;
+    if (sel && p <= q_idx) orow[pos++] = p;
+  }
   for (int i = kept + tid; i < take; i += 256) orow[i] = -1;
 }
-
 // ---------------------------------------------------------------------------
 // Split-K attention over the cache.  Workgroup (split s, row t, group g) has
 // four waves; wave w runs the pages of plan slots
@@ -351,6 +417,7 @@ __global__ __launch_bounds__(256) void ls_decode_topk_kernel(
 #define LS_DEC_VBYTES (64 * LS_DEC_VPITCH)
 #define LS_DEC_PART (16 * 128 + 32)  // floats per partial: O [16][128], m [16], l [16]
 #define LS_DEC_MAX_SPLITS 64
+#define LS_DEC_ID_REGS 4     // plan ids held in registers: topk <= 256
 
 __device__ __forceinline__ void ls_dec_wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -382,55 +449,58 @@ __global__ __launch_bounds__(256) void ls_decode_attn_kernel(
   ls_u32x4 qf[4];
   const uint16_t* qrow = q + t * qrs + ((int64_t)g * gs + r) * D + 8 * qg;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-    qf[ks] = head_ok ? ls_load16(qrow + 32 * ks) : ls_u32x4{0u, 0u, 0u, 0u};
+  for (int k4 = 0; k4 < 4; ++k4)
+    qf[k4] = head_ok ? ls_load16(qrow + 32 * k4) : ls_u32x4{0u, 0u, 0u, 0u};
   float m_run = -INFINITY, l_run = 0.f;
   ls_f32x4 o[8];
 #pragma unroll
   for (int db = 0; db < 8; ++db) o[db] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
+  // The row's plan ids, 64 per register (topk <= 64 * LS_DEC_ID_REGS).
   const int32_t* idrow = topk_idx + ((int64_t)g * total_q + t) * topk;
+  int idr[LS_DEC_ID_REGS];
+#pragma unroll
+  for (int k = 0; k < LS_DEC_ID_REGS; ++k) idr[k] = 64 * k + lane < topk ? idrow[64 * k + lane] : -1;
   const uint16_t* kseq = kc_ + (int64_t)b * cbs + (int64_t)g * D;
   const uint16_t* vseq = vc_ + (int64_t)b * cbs + (int64_t)g * D;
   const int slot0 = (4 * s + w) * ppw, slot1 = min(topk, slot0 + ppw);
   for (int slot = slot0; slot < slot1; ++slot) {
-    const int id = idrow[slot];
+    int held = idr[0];
+#pragma unroll
+    for (int k = 1; k < LS_DEC_ID_REGS; ++k)
+      if ((slot >> 6) == k) held = idr[k];
+    const int id = __builtin_amdgcn_readlane(held, slot & 63);
     if (id < 0 || (int64_t)id >= n_pages || 64LL * id >= limit) continue;
     // Skip a repeated id (the reference forms a page bitmask, so each page counts once).
     bool dup = false;
-    for (int j0 = 0; j0 < slot; j0 += 64) {
-      const int j = j0 + lane;
-      dup |= __ballot(j < slot && idrow[j] == id) != 0ull;
-    }
+#pragma unroll
+    for (int k = 0; k < LS_DEC_ID_REGS; ++k) dup |= __ballot(64 * k + lane < slot && idr[k] == id) != 0ull;
     if (dup) continue;
     const int64_t key0 = 64LL * id;
     const int64_t nvis = min((int64_t)64, limit - key0);  // visible keys of this page (> 0)
-    // Stage V (keys past nvis as zeros) into the wave's LDS, rows of 128 values.
+    // The page's K fragments and V rows are loaded together (keys past nvis as
+    // zeros).  K block kb = 2 c + nb, MFMA row R holds key 32 c + 8 (R / 4) + 4 nb + R % 4.
+    ls_u32x4 kf[4][4], vv[16];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int krow = 32 * (kb >> 1) + 8 * (r >> 2) + 4 * (kb & 1) + (r & 3);
+      const uint16_t* kp = kseq + (key0 + krow) * crs + 8 * qg;
+#pragma unroll
+      for (int k4 = 0; k4 < 4; ++k4)
+        kf[kb][k4] = krow < nvis ? ls_load16(kp + 32 * k4) : ls_u32x4{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
     for (int it = 0; it < 16; ++it) {
       const int ci = it * 64 + lane, kr = ci >> 4, c16 = ci & 15;
-      ls_u32x4 v = {0u, 0u, 0u, 0u};
-      if (kr < nvis) v = ls_load16(vseq + (key0 + kr) * crs + 8 * c16);
-      uint32_t* dst = reinterpret_cast<uint32_t*>(sv_w + kr * LS_DEC_VPITCH + 16 * c16);
-      dst[0] = v[0];
-      dst[1] = v[1];
-      dst[2] = v[2];
-      dst[3] = v[3];
+      vv[it] = kr < nvis ? ls_load16(vseq + (key0 + kr) * crs + 8 * c16) : ls_u32x4{0u, 0u, 0u, 0u};
     }
-    // Scores: key block kb = 2 c + nb, MFMA row R holds key 32 c + 8 (R / 4) + 4 nb + R % 4.
     float sv[16];
     float pm = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const int cch = kb >> 1, nb = kb & 1;
-      const int krow = 32 * cch + 8 * (r >> 2) + 4 * nb + (r & 3);
-      const bool kin = krow < nvis;
-      const uint16_t* kp = kseq + (key0 + krow) * crs + 8 * qg;
       ls_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const ls_u32x4 kf = kin ? ls_load16(kp + 32 * ks) : ls_u32x4{0u, 0u, 0u, 0u};
-        acc = LsElem<DT>::mfma(kf, qf[ks], acc);
-      }
+      for (int k4 = 0; k4 < 4; ++k4) acc = LsElem<DT>::mfma(kf[kb][k4], qf[k4], acc);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = 32 * cch + 8 * qg + 4 * nb + i;  // row 4 qg + i of block kb
@@ -438,6 +508,16 @@ __global__ __launch_bounds__(256) void ls_decode_attn_kernel(
         sv[4 * kb + i] = v;
         pm = fmaxf(pm, v);
       }
+    }
+    // V into the wave's LDS, rows of 128 values.
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      const int ci = it * 64 + lane, kr = ci >> 4, c16 = ci & 15;
+      uint32_t* dst = reinterpret_cast<uint32_t*>(sv_w + kr * LS_DEC_VPITCH + 16 * c16);
+      dst[0] = vv[it][0];
+      dst[1] = vv[it][1];
+      dst[2] = vv[it][2];
+      dst[3] = vv[it][3];
     }
     pm = fmaxf(pm, ls_shfl_xor(pm, 16));
     pm = fmaxf(pm, ls_shfl_xor(pm, 32));
@@ -522,48 +602,42 @@ __global__ __launch_bounds__(256) void ls_decode_attn_kernel(
 }
 
 // out[t][g*gs + h][:] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s; rows
-// without a visible key give zeros and lse = +inf.  The splits' weights are
-// formed once per head in LDS; each output is then a sum of independent loads.
+// without a visible key give zeros and lse = +inf.  One workgroup per (row,
+// group, head), a thread per output dimension; the first wave forms the
+// splits' normalised weights (one split per lane) in LDS.
 template <int DT>
-__global__ __launch_bounds__(256) void ls_decode_combine_kernel(
+__global__ __launch_bounds__(128) void ls_decode_combine_kernel(
     const float* __restrict__ part, int64_t total_q, int gs, int D, int n_splits,
     uint16_t* __restrict__ out, float* __restrict__ lse) {
   const int64_t t = LS_BID_X;
   const int g = LS_BID_Y;
+  const int h = LS_BID_Z;
   const int tid = LS_TID;
   const int G = gridDim.y;
-  __shared__ float s_w[LS_DEC_MAX_SPLITS][16];
-  __shared__ float s_m[LS_DEC_MAX_SPLITS][16];
-  __shared__ float s_l[LS_DEC_MAX_SPLITS][16];
-  __shared__ float s_lse[16];
+  __shared__ float s_w[LS_DEC_MAX_SPLITS];
+  __shared__ float s_lse;
   const float* pr = part + ((int64_t)g * total_q + t) * n_splits * LS_DEC_PART;
-  for (int i = tid; i < n_splits * 16; i += 256) {
-    const int sp = i >> 4, h = i & 15;
-    s_m[sp][h] = pr[sp * LS_DEC_PART + 16 * 128 + h];
-    s_l[sp][h] = pr[sp * LS_DEC_PART + 16 * 128 + 16 + h];
-  }
-  __syncthreads();
-  if (tid < 16) {
-    float M = -INFINITY;
-    for (int sp = 0; sp < n_splits; ++sp) M = fmaxf(M, s_m[sp][tid]);
-    float L = 0.f;
-    for (int sp = 0; sp < n_splits; ++sp) {
-      const float wt = s_m[sp][tid] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[sp][tid] - M);
-      s_w[sp][tid] = wt;
-      L += wt * s_l[sp][tid];
-    }
+  if (tid < 64) {
+    const float m = tid < n_splits ? pr[tid * LS_DEC_PART + 16 * 128 + h] : -INFINITY;
+    const float l = tid < n_splits ? pr[tid * LS_DEC_PART + 16 * 128 + 16 + h] : 0.f;
+    float M = m;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, ls_shfl_xor(M, o));
+    const float wt = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+    float L = wt * l;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) L += ls_shfl_xor(L, o);
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    for (int sp = 0; sp < n_splits; ++sp) s_w[sp][tid] *= inv;
-    s_lse[tid] = L > 0.f ? (M + __log2f(L)) * 0.69314718055994531f : INFINITY;
+    if (tid < n_splits) s_w[tid] = wt * inv;
+    if (tid == 0) s_lse = L > 0.f ? (M + __log2f(L)) * 0.69314718055994531f : INFINITY;
   }
   __syncthreads();
-  for (int e = tid; e < gs * 128; e += 256) {
-    const int h = e >> 7, d = e & 127;
+  for (int d = tid; d < D; d += 128) {
     float acc = 0.f;
-    for (int sp = 0; sp < n_splits; ++sp) acc += s_w[sp][h] * pr[sp * LS_DEC_PART + h * 128 + d];
+    for (int sp = 0; sp < n_splits; ++sp) acc += s_w[sp] * pr[sp * LS_DEC_PART + h * 128 + d];
     out[(t * G + g) * (int64_t)gs * D + (int64_t)h * D + d] = LsElem<DT>::from_f(acc);
-    if (lse && d == 0) lse[((int64_t)g * gs + h) * total_q + t] = s_lse[h];
   }
+  if (lse && tid == 0) lse[((int64_t)g * gs + h) * total_q + t] = s_lse;
 }
 
 // ---------------------------------------------------------------------------
@@ -630,25 +704,19 @@ extern "C" int ls_kvcache_append(void* k_cache, void* v_cache, int64_t cache_bat
 
 namespace {
 struct SelWs {
-  size_t cu_kc, cache_lens, x, part, score, pooled, total;
+  size_t x, part, pooled, total;
   int64_t ncpad;
   int n_chunks;
 };
-SelWs sel_ws(int64_t total_q, int batch, int G, int64_t max_kc, int64_t out_len) {
+SelWs sel_ws(int64_t total_q, int G, int64_t max_kc, int64_t out_len) {
   SelWs w;
   w.n_chunks = (int)((max_kc + 63) / 64);
   w.ncpad = (int64_t)w.n_chunks * 64;
   size_t off = 0;
-  w.cu_kc = off;
-  off = ls_align256(off + 4 * (size_t)(batch + 1));
-  w.cache_lens = off;
-  off = ls_align256(off + 4 * (size_t)(batch + 1));
   w.x = off;
   off = ls_align256(off + 4 * (size_t)G * total_q * 16 * w.ncpad);
   w.part = off;
   off = ls_align256(off + 4 * (size_t)G * total_q * w.n_chunks * 32);
-  w.score = off;
-  off = ls_align256(off + 2 * (size_t)G * total_q * max_kc);
   w.pooled = off;
   off = ls_align256(off + 2 * (size_t)G * total_q * out_len);
   w.total = off;
@@ -659,15 +727,9 @@ SelWs sel_ws(int64_t total_q, int batch, int G, int64_t max_kc, int64_t out_len)
 extern "C" size_t ls_decode_select_workspace_size(int64_t total_q, int32_t batch,
                                                   int32_t num_kv_heads, int64_t max_kc,
                                                   int64_t out_len) {
-  return sel_ws(total_q, batch, num_kv_heads, max_kc, out_len).total;
+  (void)batch;
+  return sel_ws(total_q, num_kv_heads, max_kc, out_len).total;
 }
-
-extern "C" int ls_page_maxpool_varlen(const void* input, const int32_t* cu_seqlens_q,
-                                      const int32_t* cu_seqlens_k, const int32_t* cache_lens,
-                                      int32_t batch, int32_t num_heads, int64_t total_q,
-                                      int64_t max_seqlen_k, int64_t out_len, int32_t local_blocks,
-                                      int32_t init_blocks, int32_t block_size, int32_t stride,
-                                      int32_t dtype, void* out, void* stream);
 
 extern "C" int ls_decode_select(const void* q, int64_t q_row_stride, const int32_t* cu_seqlens_q,
                                 int64_t total_q, const void* kc_cache, int64_t kc_batch_stride,
@@ -688,8 +750,11 @@ extern "C" int ls_decode_select(const void* q, int64_t q_row_stride, const int32
   LS_REQUIRE(block_size > 0 && kernel_stride > 0 && block_size % kernel_stride == 0 &&
                  kernel_size > 0,
              LS_ERR_INVALID, "ls_decode_select: bad page geometry");
-  LS_REQUIRE(out_len >= 1 && out_len <= 65535 && take >= 1 && take <= out_len && take <= topk,
-             LS_ERR_INVALID, "ls_decode_select: need 1 <= take <= min(topk, out_len), out_len < 65536");
+  LS_REQUIRE(out_len >= 1 && take >= 1 && take <= out_len && take <= topk, LS_ERR_INVALID,
+             "ls_decode_select: need 1 <= take <= min(topk, out_len)");
+  LS_REQUIRE(out_len <= LS_DEC_TOPK_MAX_PAGES, LS_ERR_UNSUPPORTED,
+             "ls_decode_select: at most %d pages per row (got %lld)", LS_DEC_TOPK_MAX_PAGES,
+             (long long)out_len);
   LS_REQUIRE(max_kc >= 0 && total_q <= 0x7fffffffLL && num_kv_heads <= 65535, LS_ERR_INVALID,
              "ls_decode_select: bad sizes");
   LS_REQUIRE(q_row_stride % 8 == 0 && kc_row_stride == (int64_t)num_kv_heads * head_dim &&
@@ -700,56 +765,54 @@ extern "C" int ls_decode_select(const void* q, int64_t q_row_stride, const int32
   LS_REQUIRE(q && cu_seqlens_q && cache_seqlens && topk_idx && ws, LS_ERR_INVALID,
              "ls_decode_select: null pointer");
   LS_REQUIRE(max_kc == 0 || kc_cache, LS_ERR_INVALID, "ls_decode_select: null compressed cache");
-  const SelWs L = sel_ws(total_q, batch, num_kv_heads, max_kc, out_len);
+  const int sp = block_size / kernel_stride;
+  LS_REQUIRE(sp <= 256, LS_ERR_UNSUPPORTED,
+             "ls_decode_select: at most 256 compressed keys per page (got %d)", sp);
+  const SelWs L = sel_ws(total_q, num_kv_heads, max_kc, out_len);
   LS_REQUIRE(ws_bytes >= L.total, LS_ERR_WORKSPACE, "ls_decode_select: workspace %zu < %zu",
              ws_bytes, L.total);
   uint8_t* w = (uint8_t*)ws;
-  int32_t* cu_kc = (int32_t*)(w + L.cu_kc);
-  int32_t* cache_lens = (int32_t*)(w + L.cache_lens);
   float* x = (float*)(w + L.x);
   float* part = (float*)(w + L.part);
-  uint16_t* score = (uint16_t*)(w + L.score);
   uint16_t* pooled = (uint16_t*)(w + L.pooled);
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(ls_decode_plan_kernel, dim3(1), dim3(64), 0, s, cache_seqlens, cu_seqlens_q,
-                     batch, kernel_size, kernel_stride, cu_kc, cache_lens);
-  int rc = ls_check_launch("ls_decode_plan_kernel");
-  if (rc) return rc;
   const float scale_log2 = softmax_scale * 1.4426950408889634f;
+  int rc;
   if (max_kc > 0) {
     const dim3 g1((unsigned)L.n_chunks, (unsigned)total_q, num_kv_heads);
-    const dim3 g2((unsigned)total_q, num_kv_heads);
-    if (dtype == LS_BF16) {
+    if (dtype == LS_BF16)
       hipLaunchKernelGGL(ls_stage1_chunk_kernel<LS_BF16>, g1, dim3(64), 0, s, (const uint16_t*)q,
                          q_row_stride, cu_seqlens_q, batch, total_q, (const uint16_t*)kc_cache,
-                         kc_batch_stride, kc_row_stride, cu_kc, gs, head_dim, scale_log2, L.ncpad,
-                         L.n_chunks, x, part);
-      rc = ls_check_launch("ls_stage1_chunk_kernel");
-      if (rc) return rc;
-      hipLaunchKernelGGL(ls_stage1_finish_kernel<LS_BF16>, g2, dim3(256), 0, s, x, part,
-                         cu_seqlens_q, batch, total_q, cu_kc, gs, L.ncpad, L.n_chunks, max_kc,
-                         score);
-    } else {
+                         kc_batch_stride, kc_row_stride, cache_seqlens, kernel_size,
+                         kernel_stride, max_kc, gs, head_dim, scale_log2, L.ncpad, L.n_chunks, x,
+                         part);
+    else
       hipLaunchKernelGGL(ls_stage1_chunk_kernel<LS_F16>, g1, dim3(64), 0, s, (const uint16_t*)q,
                          q_row_stride, cu_seqlens_q, batch, total_q, (const uint16_t*)kc_cache,
-                         kc_batch_stride, kc_row_stride, cu_kc, gs, head_dim, scale_log2, L.ncpad,
-                         L.n_chunks, x, part);
-      rc = ls_check_launch("ls_stage1_chunk_kernel");
-      if (rc) return rc;
-      hipLaunchKernelGGL(ls_stage1_finish_kernel<LS_F16>, g2, dim3(256), 0, s, x, part,
-                         cu_seqlens_q, batch, total_q, cu_kc, gs, L.ncpad, L.n_chunks, max_kc,
-                         score);
-    }
-    rc = ls_check_launch("ls_stage1_finish_kernel");
+                         kc_batch_stride, kc_row_stride, cache_seqlens, kernel_size,
+                         kernel_stride, max_kc, gs, head_dim, scale_log2, L.ncpad, L.n_chunks, x,
+                         part);
+    rc = ls_check_launch("ls_stage1_chunk_kernel");
     if (rc) return rc;
   }
-  rc = ls_page_maxpool_varlen(score, cu_seqlens_q, cu_kc, cache_lens, batch, num_kv_heads,
-                              total_q, max_kc, out_len, local_blocks, init_blocks, block_size,
-                              kernel_stride, LS_BF16, pooled, stream);
+  const int ppb = 256 / sp;
+  const dim3 g2((unsigned)((out_len + ppb - 1) / ppb), (unsigned)total_q, num_kv_heads);
+  if (dtype == LS_BF16)
+    hipLaunchKernelGGL(ls_stage1_pool_kernel<LS_BF16>, g2, dim3(256), 0, s, x, part, cu_seqlens_q,
+                       batch, total_q, cache_seqlens, kernel_size, kernel_stride, max_kc, gs,
+                       L.ncpad, L.n_chunks, sp, ppb, out_len, block_size, init_blocks,
+                       local_blocks, pooled);
+  else
+    hipLaunchKernelGGL(ls_stage1_pool_kernel<LS_F16>, g2, dim3(256), 0, s, x, part, cu_seqlens_q,
+                       batch, total_q, cache_seqlens, kernel_size, kernel_stride, max_kc, gs,
+                       L.ncpad, L.n_chunks, sp, ppb, out_len, block_size, init_blocks,
+                       local_blocks, pooled);
+  rc = ls_check_launch("ls_stage1_pool_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(ls_decode_topk_kernel, dim3((unsigned)total_q, num_kv_heads), dim3(256), 0,
-                     s, pooled, cu_seqlens_q, batch, total_q, cache_lens, (int)out_len,
-                     block_size, take, topk_idx);
+  const size_t key_bytes = ((size_t)out_len * 2 + 3) & ~(size_t)3;
+  hipLaunchKernelGGL(ls_decode_topk_kernel, dim3((unsigned)total_q, num_kv_heads), dim3(256),
+                     key_bytes, s, pooled, cu_seqlens_q, batch, total_q, cache_seqlens,
+                     (int)out_len, block_size, take, topk_idx);
   return ls_check_launch("ls_decode_topk_kernel");
 }
 
@@ -778,6 +841,9 @@ extern "C" int ls_sparse_attn_kvcache(const void* q, int64_t q_row_stride,
              "ls_sparse_attn_kvcache: bf16 or fp16");
   LS_REQUIRE(topk >= 1 && n_splits >= 1 && n_splits <= LS_DEC_MAX_SPLITS, LS_ERR_INVALID,
              "ls_sparse_attn_kvcache: need topk >= 1 and 1 <= n_splits <= %d", LS_DEC_MAX_SPLITS);
+  LS_REQUIRE(topk <= 64 * LS_DEC_ID_REGS, LS_ERR_UNSUPPORTED,
+             "ls_sparse_attn_kvcache: at most %d plan ids per row (got %d)", 64 * LS_DEC_ID_REGS,
+             topk);
   LS_REQUIRE(total_q <= 0x7fffffffLL && num_kv_heads <= 65535, LS_ERR_INVALID,
              "ls_sparse_attn_kvcache: too many rows or heads");
   LS_REQUIRE(q_row_stride % 8 == 0 && cache_row_stride % 8 == 0 && cache_batch_stride % 8 == 0,
@@ -797,7 +863,7 @@ extern "C" int ls_sparse_attn_kvcache(const void* q, int64_t q_row_stride,
   const float scale_log2 = softmax_scale * 1.4426950408889634f;
   float* part = (float*)ws;
   const dim3 grid((unsigned)splits, (unsigned)total_q, num_kv_heads);
-  const dim3 cgrid((unsigned)total_q, num_kv_heads);
+  const dim3 cgrid((unsigned)total_q, num_kv_heads, gs);
   if (dtype == LS_BF16) {
     hipLaunchKernelGGL(ls_decode_attn_kernel<LS_BF16>, grid, dim3(256), 0, s, (const uint16_t*)q,
                        q_row_stride, cu_seqlens_q, batch, total_q, (const uint16_t*)k_cache,
@@ -806,7 +872,7 @@ extern "C" int ls_sparse_attn_kvcache(const void* q, int64_t q_row_stride,
                        causal, part);
     int rc = ls_check_launch("ls_decode_attn_kernel");
     if (rc) return rc;
-    hipLaunchKernelGGL(ls_decode_combine_kernel<LS_BF16>, cgrid, dim3(256), 0, s, part, total_q,
+    hipLaunchKernelGGL(ls_decode_combine_kernel<LS_BF16>, cgrid, dim3(128), 0, s, part, total_q,
                        gs, head_dim, splits, (uint16_t*)out, softmax_lse);
   } else {
     hipLaunchKernelGGL(ls_decode_attn_kernel<LS_F16>, grid, dim3(256), 0, s, (const uint16_t*)q,
@@ -816,7 +882,7 @@ extern "C" int ls_sparse_attn_kvcache(const void* q, int64_t q_row_stride,
                        causal, part);
     int rc = ls_check_launch("ls_decode_attn_kernel");
     if (rc) return rc;
-    hipLaunchKernelGGL(ls_decode_combine_kernel<LS_F16>, cgrid, dim3(256), 0, s, part, total_q,
+    hipLaunchKernelGGL(ls_decode_combine_kernel<LS_F16>, cgrid, dim3(128), 0, s, part, total_q,
                        gs, head_dim, splits, (uint16_t*)out, softmax_lse);
   }
   return ls_check_launch("ls_decode_combine_kernel");

@@ -174,8 +174,8 @@ def sparse_attention_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
     B, cap, G, Dk = k_cache.shape
     if Dk != D or H % G or q.dtype != k_cache.dtype:
         raise ValueError("q and the cache must share head_dim and dtype, H divisible by G")
-    if topk_idx.shape[0] != G or topk_idx.shape[1] != total_q or topk_idx.shape[2] < 1:
-        raise ValueError(f"topk_idx must be [{G}, {total_q}, k >= 1]")
+    if topk_idx.shape[0] != G or topk_idx.shape[1] != total_q or not 1 <= topk_idx.shape[2] <= 256:
+        raise ValueError(f"topk_idx must be [{G}, {total_q}, k] with 1 <= k <= 256")
     if cache_seqlens.dtype != torch.int32 or cache_seqlens.numel() != B \
             or cu_seqlens_q.dtype != torch.int32 or cu_seqlens_q.numel() != B + 1:
         raise ValueError("cache_seqlens must be int32 [batch] and cu_seqlens_q int32 [batch + 1]")
