@@ -477,7 +477,7 @@ def model_bench(args, dev) -> None:
     assert bool(torch.isfinite(logits).all()), "non-finite logits"
 
     # Stage breakdown of layer 0 (HIP events on the launch stream).
-    from leanselect_amd.ops import compress_k, leanselect_prefill_topk_idx, sparse_attention
+    from leanselect_amd.ops import leanselect_prefill_topk_idx, sparse_attention
 
     it = args.kernel_iters
     H, G, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
@@ -488,14 +488,17 @@ def model_bench(args, dev) -> None:
     h = minicpm.rms_layernorm(x, L.input_norm, cfg.rms_norm_eps)
     qkv = F.linear(h, L.w_qkv)
     cos, sin = model.rope_tables(max(wl["seq_lens"]))
-    minicpm.rope_inplace(qkv, pos, cos, sin, n_q_heads=H, n_k_heads=G, k_col_offset=H * D)
+    # As the model's attention runs it: the query heads rotate in the pass that
+    # forms q~, the key heads in the pass that forms the compressed keys.
+    qt = minicpm.rope_project_queries(qkv, pos, cos, sin, L.selector, n_q_heads=H, head_dim=D)
+    kc, cu_c = minicpm.rope_k_compress(qkv, pos, cos, sin, cu, cu_host, n_k_heads=G,
+                                       k_col_offset=H * D, head_dim=D)
     q = qkv[:, :H * D].view(N, H, D)
     k = qkv[:, H * D:H * D + G * D].view(N, G, D)
     v = qkv[:, H * D + G * D:].view(N, G, D)
-    kc, cu_c = compress_k(k, cu, cu_seqlens_host=cu_host)
     kw = dict(topk=cfg.topk, init_blocks=cfg.init_blocks, local_blocks=cfg.local_blocks,
               cu_seqlens_q_host=cu_host)
-    sel_ids = leanselect_prefill_topk_idx(q, kc, cu, cu_c, L.selector, **kw)
+    sel_ids = leanselect_prefill_topk_idx(q, kc, cu, cu_c, L.selector, q_tilde=qt, **kw)
     attn = sparse_attention(q, k, v, cu, cu, N, N, sel_ids)
     o = F.linear(attn.view(N, H * D), L.w_o)
     gu = F.linear(h, L.w_gate_up)
@@ -504,12 +507,13 @@ def model_bench(args, dev) -> None:
     stages = {
         "rmsnorm": lambda: minicpm.rms_layernorm(x, L.input_norm, cfg.rms_norm_eps, out=h),
         "qkv_gemm": lambda: F.linear(h, L.w_qkv),
-        "rope_q": lambda: minicpm.rope_inplace(qkv, pos, cos, sin, n_q_heads=H, n_k_heads=0,
-                                               k_col_offset=H * D, check_positions=False),
+        "rope_q_project": lambda: minicpm.rope_project_queries(
+            qkv, pos, cos, sin, L.selector, n_q_heads=H, head_dim=D, check_positions=False),
         "rope_k_compress": lambda: minicpm.rope_k_compress(
             qkv, pos, cos, sin, cu, cu_host, n_k_heads=G, k_col_offset=H * D,
             check_positions=False),
-        "select": lambda: leanselect_prefill_topk_idx(q, kc, cu, cu_c, L.selector, **kw),
+        "select": lambda: leanselect_prefill_topk_idx(q, kc, cu, cu_c, L.selector, q_tilde=qt,
+                                                      **kw),
         "sparse_attention": lambda: sparse_attention(q, k, v, cu, cu, N, N, sel_ids),
         "o_gemm": lambda: F.linear(attn.view(N, H * D), L.w_o),
         "add_rmsnorm": lambda: minicpm.add_rms_layernorm(xs, o, 0.0, L.post_norm, cfg.rms_norm_eps, out=h),

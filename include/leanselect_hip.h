@@ -96,6 +96,26 @@ int ls_project_queries(const void* query, int64_t q_row_stride, int64_t total_q,
                        size_t workspace_bytes, void* stream);
 
 /*
+ * Rotary embedding of the query heads fused with ls_project_queries: the H
+ * query heads of query [total_q, H, D] (rows q_row_stride elements apart) are
+ * rotated in place exactly as ls_rope_inplace rotates them (positions int32,
+ * cos_table / sin_table float32 [table_rows, 128]), and out [G, total_q, R*F]
+ * is the projection of the rotated rows, bit-identical to calling
+ * ls_rope_inplace and then ls_project_queries.  bf16 or fp16, head_dim 128,
+ * router width R*F 64 or 128.  Workspace as for ls_project_queries.
+ * Replaces apply_rotary_pos_emb on the queries (leanselect/models/minicpm.py:
+ * 1027-1070, called at 2219-2222) followed by LeanSelectSelector.project_queries
+ * on the rotated queries (selector.py:160-177, reached from minicpm.py:
+ * 2504-2508 and 3061-3142): the projection no longer reads the queries again.
+ */
+int ls_rope_project_queries(void* query, int64_t q_row_stride, const int32_t* positions,
+                            int64_t total_q, int32_t num_heads, int32_t num_kv_heads,
+                            int32_t head_dim, const float* cos_table, const float* sin_table,
+                            int64_t table_rows, const float* head_mix, const float* q_proj,
+                            int32_t router_heads, int32_t router_dim, int32_t dtype, void* out,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Atom-key projection: out[g, a, f] = sum_d kc[a, g, d] * kv_fused[g, d, f].
  *   kc [n_atoms, G, D] with rows `kc_row_stride` elements apart; out [G, n_atoms, R*F].
  * Replaces LeanSelectSelector.project_atom_keys (leanselect/selector.py:179-190).
@@ -165,6 +185,25 @@ int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t total_q, cons
                       int32_t dtype, int32_t topk, int32_t block_size, int32_t kernel_stride,
                       int32_t init_blocks, int32_t local_blocks, int32_t* topk_idx,
                       int32_t take, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * ls_select_prefill with the query projection q_tilde [G, total_q, R*F]
+ * (dtype, dense) given instead of the queries, e.g. from
+ * ls_rope_project_queries; only the key-side masters (kv_head_mix, k_proj)
+ * are read.  Same plans as ls_select_prefill on the queries q_tilde was
+ * projected from.
+ * Replaces the same selection (leanselect/models/minicpm.py:3061-3142) with
+ * its q~ produced where the queries are rotated (minicpm.py:2219-2222).
+ */
+int ls_select_prefill_qt(const void* q_tilde, int64_t total_q, const void* kc,
+                         int64_t kc_row_stride, int64_t total_atoms, const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_kc, int32_t batch, int32_t max_seqlen_q,
+                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                         const float* kv_head_mix, const float* k_proj, int32_t router_heads,
+                         int32_t router_dim, int32_t dtype, int32_t topk, int32_t block_size,
+                         int32_t kernel_stride, int32_t init_blocks, int32_t local_blocks,
+                         int32_t* topk_idx, int32_t take, void* workspace,
+                         size_t workspace_bytes, void* stream);
 
 /*
  * Workspace bytes needed by ls_sparse_attn_varlen.

@@ -31,6 +31,9 @@ SIGNATURES = {
         _sz, [_i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "ls_project_queries": (
         _i32, [_p, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _i32, _p, _p, _sz, _p]),
+    "ls_rope_project_queries": (
+        _i32, [_p, _i64, _p, _i64, _i32, _i32, _i32, _p, _p, _i64, _p, _p, _i32, _i32, _i32, _p,
+               _p, _sz, _p]),
     "ls_project_atom_keys": (
         _i32, [_p, _i64, _i64, _i32, _i32, _p, _p, _i32, _i32, _i32, _p, _p, _sz, _p]),
     "ls_score_pages": (
@@ -41,6 +44,9 @@ SIGNATURES = {
     "ls_select_prefill": (
         _i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p,
                _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i32, _p, _sz, _p]),
+    "ls_select_prefill_qt": (
+        _i32, [_p, _i64, _p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _i32, _i32,
+               _i32, _i32, _i32, _i32, _i32, _i32, _p, _i32, _p, _sz, _p]),
     "ls_sparse_attn_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32]),
     "ls_attn_set_spin_limit": (_i32, [_i32]),
     "ls_sparse_attn_varlen_noalloc": (

@@ -201,6 +201,155 @@ __global__ __launch_bounds__(256, 2) void ls_proj_tile_kernel(
   }
 }
 
+// Rotary embedding of the query heads fused with the q~ projection
+// (producer-side: the rotated rows feed the projection's MFMAs from registers,
+// so the projection does not read the queries a second time).  Rotation as
+// apply_rotary_pos_emb (leanselect/models/minicpm.py:1027-1070):
+//   y[d] = round(x[d] cos[p][d] - x[d + 64] sin[p][d]),
+//   y[d + 64] = round(x[d + 64] cos[p][d + 64] + x[d] sin[p][d + 64])  (d < 64)
+// with every product and sum rounded to float32 (no fused multiply-add), the
+// rotated values written back in place, and the projection computed exactly as
+// ls_proj_tile_kernel computes it (same K-step and slice order), so q~ is
+// bit-identical to rotating first and projecting after.  A workgroup owns 128
+// rows (eight waves of 16, sharing each K step's weight tile in LDS) of one KV
+// group; in slice ks of a K step (one head) lane
+// group q holds dims 32 ks + 8 q .. +7, so the rotation pairs (ks, ks + 2) sit
+// in the same lane, and each lane keeps its row's 64 rotary coefficients.
+__device__ __forceinline__ void ls_rope_pair(float x1, float x2, float c1, float c2, float s1,
+                                             float s2, float& y1, float& y2) {
+#pragma clang fp contract(off)
+  y1 = x1 * c1 + (-x2) * s1;
+  y2 = x2 * c2 + x1 * s2;
+}
+
+#define LS_RP_WAVES 8  // waves (16 rows each) per workgroup of the fused rotary projection
+
+template <int DT, int FB>
+__global__ __launch_bounds__(64 * LS_RP_WAVES, 1) void ls_rope_proj_kernel(
+    uint16_t* __restrict__ A, int64_t lda, int gs, int64_t M, const int32_t* __restrict__ pos,
+    const float* __restrict__ cosb, const float* __restrict__ sinb, int64_t table_rows,
+    const uint16_t* __restrict__ wt, uint16_t* __restrict__ out) {
+  constexpr int F = FB * 16;
+  constexpr int NT = 64 * LS_RP_WAVES;
+  constexpr int NB = F * 16 / NT;  // 16-byte weight chunks per thread per K step
+  static_assert(NB * NT == F * 16, "weight tile must split evenly over the threads");
+  __shared__ ls_u32x4 sB[2][F * 16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int g = blockIdx.y;
+  const int64_t m0 = (int64_t)blockIdx.x * (16 * LS_RP_WAVES) + w * 16;  // the wave's first row
+  const int64_t row = m0 + r;                             // this lane's A row
+  const bool row_ok = row < M;
+  const int64_t rowc = row_ok ? row : M - 1;
+  const int K = gs * 128, nk = gs;
+  uint16_t* ap = A + rowc * lda + (int64_t)g * K + 8 * q;
+  const uint16_t* Wg = wt + (int64_t)g * F * K;
+
+  int64_t p = pos[rowc];
+  p = p < 0 ? 0 : (p >= table_rows ? table_rows - 1 : p);  // the host checks the range
+  float c1[2][8], c2[2][8], s1[2][8], s2[2][8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t d0 = p * 128 + 32 * h + 8 * q;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const ls_f32x4 a = *reinterpret_cast<const ls_f32x4*>(cosb + d0 + 4 * i);
+      const ls_f32x4 b = *reinterpret_cast<const ls_f32x4*>(cosb + d0 + 64 + 4 * i);
+      const ls_f32x4 e = *reinterpret_cast<const ls_f32x4*>(sinb + d0 + 4 * i);
+      const ls_f32x4 f = *reinterpret_cast<const ls_f32x4*>(sinb + d0 + 64 + 4 * i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c1[h][4 * i + j] = a[j];
+        c2[h][4 * i + j] = b[j];
+        s1[h][4 * i + j] = e[j];
+        s2[h][4 * i + j] = f[j];
+      }
+    }
+  }
+
+  ls_u32x4 breg[NB];
+  auto load_b = [&](int kt) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int i = tid + NT * j, f = i >> 4, ch = i & 15;
+      breg[j] = ls_load16(Wg + (int64_t)f * K + 128 * kt + 8 * ch);
+    }
+  };
+  auto store_b = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int i = tid + NT * j, f = i >> 4, ch = i & 15;
+      sB[buf][f * 16 + (ch ^ (f & 15))] = breg[j];
+    }
+  };
+  ls_u32x4 a[4];  // the row's slices of the next K step (in flight while one is rotated)
+  auto load_a = [&](int kt) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) a[ks] = ls_load16(ap + 128 * kt + 32 * ks);
+  };
+
+  ls_f32x4 acc[FB];
+#pragma unroll
+  for (int c = 0; c < FB; ++c) acc[c] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
+  load_b(0);
+  load_a(0);
+  store_b(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    ls_u32x4 x[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) x[ks] = a[ks];
+    if (kt + 1 < nk) {
+      load_b(kt + 1);
+      load_a(kt + 1);
+    }
+    // Rotate the head's slices (pairs ks, ks + 2) and write them back.
+    ls_u32x4 y[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float lo1, hi1, lo2, hi2;
+        const float xa0 = LsElem<DT>::to_f((uint16_t)(x[h][e] & 0xffffu));
+        const float xa1 = LsElem<DT>::to_f((uint16_t)(x[h][e] >> 16));
+        const float xb0 = LsElem<DT>::to_f((uint16_t)(x[h + 2][e] & 0xffffu));
+        const float xb1 = LsElem<DT>::to_f((uint16_t)(x[h + 2][e] >> 16));
+        ls_rope_pair(xa0, xb0, c1[h][2 * e], c2[h][2 * e], s1[h][2 * e], s2[h][2 * e], lo1, lo2);
+        ls_rope_pair(xa1, xb1, c1[h][2 * e + 1], c2[h][2 * e + 1], s1[h][2 * e + 1],
+                     s2[h][2 * e + 1], hi1, hi2);
+        y[h][e] = ls_pack2(LsElem<DT>::from_f(lo1), LsElem<DT>::from_f(hi1));
+        y[h + 2][e] = ls_pack2(LsElem<DT>::from_f(lo2), LsElem<DT>::from_f(hi2));
+      }
+    }
+    if (row_ok) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        *reinterpret_cast<ls_u32x4*>(ap + 128 * kt + 32 * ks) = y[ks];
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int c = 0; c < FB; ++c) {
+        const ls_u32x4 b = sB[buf][(16 * c + r) * 16 + ((4 * ks + q) ^ r)];
+        acc[c] = LsElem<DT>::mfma(y[ks], b, acc[c]);
+      }
+    }
+    if (kt + 1 < nk) store_b(buf ^ 1);
+    __syncthreads();
+  }
+  if (m0 >= M) return;
+  uint16_t* og = out + (int64_t)g * M * F;
+#pragma unroll
+  for (int c = 0; c < FB; ++c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t mo = m0 + 4 * q + i;
+      if (mo < M) og[mo * F + c * 16 + r] = LsElem<DT>::from_f(acc[c][i]);
+    }
+  }
+}
+
 // float32 projection on the vector ALU (the reference's float32 path).
 __global__ __launch_bounds__(256) void ls_proj_f32_kernel(
     const float* __restrict__ A, int64_t lda, int64_t gk, int64_t M, int K, int F,
@@ -1152,6 +1301,62 @@ extern "C" int ls_project_queries(const void* query, int64_t q_row_stride, int64
                  G, ws + L.wq, out, s);
 }
 
+extern "C" int ls_rope_project_queries(void* query, int64_t q_row_stride,
+                                       const int32_t* positions, int64_t total_q,
+                                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                       const float* cos_table, const float* sin_table,
+                                       int64_t table_rows, const float* head_mix,
+                                       const float* q_proj, int32_t router_heads,
+                                       int32_t router_dim, int32_t dtype, void* out,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_dims("ls_rope_project_queries", num_heads, num_kv_heads, head_dim, router_heads,
+                      router_dim, dtype);
+  if (rc) return rc;
+  const int F = router_heads * router_dim, G = num_kv_heads, gs = num_heads / num_kv_heads;
+  LS_REQUIRE(dtype == LS_BF16 || dtype == LS_F16, LS_ERR_UNSUPPORTED,
+             "ls_rope_project_queries: bf16 or fp16 queries");
+  LS_REQUIRE(head_dim == 128 && (F == 64 || F == 128), LS_ERR_UNSUPPORTED,
+             "ls_rope_project_queries: head_dim 128 and router width 64 or 128 (got %d, %d)",
+             head_dim, F);
+  LS_REQUIRE(total_q >= 0 && table_rows > 0 && q_row_stride % 8 == 0 &&
+                 q_row_stride >= (int64_t)num_heads * head_dim,
+             LS_ERR_INVALID, "ls_rope_project_queries: bad sizes or row stride");
+  if (total_q == 0) return LS_OK;
+  LS_REQUIRE(query && positions && cos_table && sin_table && out, LS_ERR_INVALID,
+             "ls_rope_project_queries: null tensor");
+  LS_REQUIRE(ls_aligned16(query) && ls_aligned16(cos_table) && ls_aligned16(sin_table),
+             LS_ERR_UNSUPPORTED, "ls_rope_project_queries: tensors must be 16-byte aligned");
+  const int eb = (int)ls_dtype_bytes(dtype);
+  const WsLayout L = ws_layout(0, 0, 0, num_heads, G, head_dim, F, 0, eb);
+  LS_REQUIRE(workspace && workspace_bytes >= L.total, LS_ERR_WORKSPACE,
+             "ls_rope_project_queries: workspace needs %zu bytes", L.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  rc = fuse_t(dtype, head_mix, q_proj, G, gs, router_heads, head_dim, router_dim, ws + L.wq, s);
+  if (rc) return rc;
+  const dim3 grid((unsigned)((total_q + 16 * LS_RP_WAVES - 1) / (16 * LS_RP_WAVES)), G);
+  const dim3 block(64 * LS_RP_WAVES);
+  uint16_t* x = (uint16_t*)query;
+  const uint16_t* w = (const uint16_t*)(ws + L.wq);
+  uint16_t* o = (uint16_t*)out;
+  if (dtype == LS_BF16) {
+    if (F == 64)
+      hipLaunchKernelGGL((ls_rope_proj_kernel<LS_BF16, 4>), grid, block, 0, s, x, q_row_stride,
+                         gs, total_q, positions, cos_table, sin_table, table_rows, w, o);
+    else
+      hipLaunchKernelGGL((ls_rope_proj_kernel<LS_BF16, 8>), grid, block, 0, s, x, q_row_stride,
+                         gs, total_q, positions, cos_table, sin_table, table_rows, w, o);
+  } else {
+    if (F == 64)
+      hipLaunchKernelGGL((ls_rope_proj_kernel<LS_F16, 4>), grid, block, 0, s, x, q_row_stride,
+                         gs, total_q, positions, cos_table, sin_table, table_rows, w, o);
+    else
+      hipLaunchKernelGGL((ls_rope_proj_kernel<LS_F16, 8>), grid, block, 0, s, x, q_row_stride,
+                         gs, total_q, positions, cos_table, sin_table, table_rows, w, o);
+  }
+  return ls_check_launch("ls_rope_proj_kernel");
+}
+
 extern "C" int ls_project_atom_keys(const void* kc, int64_t kc_row_stride, int64_t n_atoms,
                                     int32_t num_kv_heads, int32_t head_dim,
                                     const float* kv_head_mix, const float* k_proj,
@@ -1219,7 +1424,8 @@ extern "C" int ls_score_pages(const void* query, int64_t q_row_stride, int64_t n
                       n_pages, G, s);
 }
 
-extern "C" int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t total_q,
+static int select_prefill_impl(const char* who, const void* q, int64_t q_row_stride,
+                               const void* q_tilde, int64_t total_q,
                                  const void* kc, int64_t kc_row_stride, int64_t total_atoms,
                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kc,
                                  int32_t batch, int32_t max_seqlen_q, int32_t num_heads,
@@ -1230,40 +1436,44 @@ extern "C" int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t to
                                  int32_t kernel_stride, int32_t init_blocks,
                                  int32_t local_blocks, int32_t* topk_idx, int32_t take,
                                  void* workspace, size_t workspace_bytes, void* stream) {
-  int rc = check_dims("ls_select_prefill", num_heads, num_kv_heads, head_dim, router_heads,
+  int rc = check_dims(who, num_heads, num_kv_heads, head_dim, router_heads,
                       router_dim, dtype);
   if (rc) return rc;
   LS_REQUIRE(batch >= 0 && total_q >= 0 && total_atoms >= 0 && max_seqlen_q >= 0, LS_ERR_INVALID,
-             "ls_select_prefill: bad sizes");
+             "%s: bad sizes", who);
   LS_REQUIRE(block_size > 0 && kernel_stride > 0 && block_size % kernel_stride == 0,
-             LS_ERR_INVALID, "ls_select_prefill: bad page geometry");
+             LS_ERR_INVALID, "%s: bad page geometry", who);
   LS_REQUIRE(init_blocks >= 0 && local_blocks >= 0 && topk >= 0, LS_ERR_INVALID,
-             "ls_select_prefill: init_blocks, local_blocks and topk must be >= 0");
+             "%s: init_blocks, local_blocks and topk must be >= 0", who);
   const int max_pages = (max_seqlen_q + block_size - 1) / block_size;
   LS_REQUIRE(take == (topk < max_pages ? topk : max_pages), LS_ERR_INVALID,
-             "ls_select_prefill: take must be min(topk, ceil(max_seqlen_q / block_size)) = %d",
+             "%s: take must be min(topk, ceil(max_seqlen_q / block_size)) = %d", who,
              topk < max_pages ? topk : max_pages);
   if (total_q == 0 || batch == 0 || take == 0) return LS_OK;
   // kc may be null only when there is no compressed key at all (every sequence
   // shorter than one window: its rows get no pages, as the reference skips it).
-  LS_REQUIRE(q && (kc || total_atoms == 0) && cu_seqlens_q && cu_seqlens_kc && topk_idx,
-             LS_ERR_INVALID, "ls_select_prefill: null pointer");
+  LS_REQUIRE((q || q_tilde) && (kc || total_atoms == 0) && cu_seqlens_q && cu_seqlens_kc &&
+                 topk_idx,
+             LS_ERR_INVALID, "%s: null pointer", who);
   const int eb = (int)ls_dtype_bytes(dtype);
   const int F = router_heads * router_dim, G = num_kv_heads, gs = num_heads / num_kv_heads;
   const WsLayout L = ws_layout(total_q, total_atoms, batch, num_heads, G, head_dim, F,
                                max_pages, eb);
   LS_REQUIRE(workspace && workspace_bytes >= L.total, LS_ERR_WORKSPACE,
-             "ls_select_prefill: workspace needs %zu bytes", L.total);
+             "%s: workspace needs %zu bytes", who, L.total);
   hipStream_t s = (hipStream_t)stream;
   char* ws = (char*)workspace;
   int32_t* blk = (int32_t*)(ws + L.blk);
-  if ((rc = fuse_t(dtype, head_mix, q_proj, G, gs, router_heads, head_dim, router_dim,
-                   ws + L.wq, s)))
+  // q~ is either given (projected where the queries were produced) or formed here.
+  if (!q_tilde && (rc = fuse_t(dtype, head_mix, q_proj, G, gs, router_heads, head_dim,
+                               router_dim, ws + L.wq, s)))
     return rc;
   if ((rc = fuse_t(dtype, kv_head_mix, k_proj, G, 1, router_heads, head_dim, router_dim,
                    ws + L.wk, s)))
     return rc;
-  if ((rc = project(dtype, q, q_row_stride, (int64_t)gs * head_dim, total_q, gs * head_dim, F,
+  const void* qt = q_tilde ? q_tilde : (const void*)(ws + L.qt);
+  if (!q_tilde &&
+      (rc = project(dtype, q, q_row_stride, (int64_t)gs * head_dim, total_q, gs * head_dim, F,
                     G, ws + L.wq, ws + L.qt, s)))
     return rc;
   if (total_atoms > 0 &&
@@ -1275,7 +1485,7 @@ extern "C" int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t to
   if ((rc = ls_check_launch("ls_select_plan_kernel"))) return rc;
   const int64_t n_blk_launch = (total_q + block_size - 1) / block_size + batch;
   if (total_atoms > 0 &&
-      (rc = score<LS_SCORE_SELECT>(dtype, F, ws + L.qt, total_q, ws + L.kt, total_atoms, cu_seqlens_q,
+      (rc = score<LS_SCORE_SELECT>(dtype, F, qt, total_q, ws + L.kt, total_atoms, cu_seqlens_q,
                         cu_seqlens_kc, blk, batch, n_blk_launch, init_blocks, local_blocks,
                         block_size, kernel_stride, 0, max_pages, ws + L.p, L.p_stride, G, s)))
     return rc;
@@ -1287,6 +1497,44 @@ extern "C" int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t to
   return launch_topk<false>(max_pages, grid, s, ws + L.p, L.p_stride, cu_seqlens_q,
                             cu_seqlens_kc, batch, total_q, G, take, init_blocks, local_blocks,
                             block_size, topk_idx);
+}
+
+extern "C" int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t total_q,
+                                 const void* kc, int64_t kc_row_stride, int64_t total_atoms,
+                                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kc,
+                                 int32_t batch, int32_t max_seqlen_q, int32_t num_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, const float* head_mix,
+                                 const float* kv_head_mix, const float* q_proj,
+                                 const float* k_proj, int32_t router_heads, int32_t router_dim,
+                                 int32_t dtype, int32_t topk, int32_t block_size,
+                                 int32_t kernel_stride, int32_t init_blocks,
+                                 int32_t local_blocks, int32_t* topk_idx, int32_t take,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  return select_prefill_impl("ls_select_prefill", q, q_row_stride, nullptr, total_q, kc,
+                             kc_row_stride, total_atoms, cu_seqlens_q, cu_seqlens_kc, batch,
+                             max_seqlen_q, num_heads, num_kv_heads, head_dim, head_mix,
+                             kv_head_mix, q_proj, k_proj, router_heads, router_dim, dtype, topk,
+                             block_size, kernel_stride, init_blocks, local_blocks, topk_idx, take,
+                             workspace, workspace_bytes, stream);
+}
+
+extern "C" int ls_select_prefill_qt(const void* q_tilde, int64_t total_q, const void* kc,
+                                    int64_t kc_row_stride, int64_t total_atoms,
+                                    const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kc,
+                                    int32_t batch, int32_t max_seqlen_q, int32_t num_heads,
+                                    int32_t num_kv_heads, int32_t head_dim,
+                                    const float* kv_head_mix, const float* k_proj,
+                                    int32_t router_heads, int32_t router_dim, int32_t dtype,
+                                    int32_t topk, int32_t block_size, int32_t kernel_stride,
+                                    int32_t init_blocks, int32_t local_blocks, int32_t* topk_idx,
+                                    int32_t take, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  return select_prefill_impl("ls_select_prefill_qt", nullptr, 0, q_tilde, total_q, kc,
+                             kc_row_stride, total_atoms, cu_seqlens_q, cu_seqlens_kc, batch,
+                             max_seqlen_q, num_heads, num_kv_heads, head_dim, nullptr,
+                             kv_head_mix, nullptr, k_proj, router_heads, router_dim, dtype, topk,
+                             block_size, kernel_stride, init_blocks, local_blocks, topk_idx, take,
+                             workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t ls_nosa_select_workspace_size(int64_t total_q, int64_t total_atoms,

@@ -50,6 +50,7 @@ __all__ = [
     "add_rms_layernorm",
     "rope_inplace",
     "rope_k_compress",
+    "rope_project_queries",
     "silu_mul",
     "embed_scale",
 ]
@@ -224,6 +225,48 @@ def rope_k_compress(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
     return kc, cu_c
 
 
+def rope_project_queries(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
+                         sin: torch.Tensor, selector, *, n_q_heads: int, head_dim: int = 128,
+                         check_positions: bool = True) -> torch.Tensor:
+    """Rotate the query heads of ``x [n, width]`` in place (as :func:`rope_inplace`)
+    and return the selector's query projection of the rotated rows,
+    ``q~ [G, n, R*F]`` -- ``LeanSelectSelector.project_queries`` (selector.py:160-177)
+    formed in the same pass, so the selection does not read the queries again.
+    bf16/fp16, ``head_dim`` 128, router width 64 or 128."""
+    from .ops.select import _masters
+
+    _rows(x, "x")
+    dev = _hip.require_gpu(x, positions, cos, sin)
+    if positions.dtype != torch.int32 or positions.shape != (x.shape[0],):
+        raise ValueError("positions must be int32 [n]")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape \
+            or cos.ndim != 2 or cos.shape[1] != head_dim:
+        raise ValueError("cos/sin must be float32 [table_rows, head_dim]")
+    if x.shape[1] < n_q_heads * head_dim:
+        raise ValueError("the query heads must lie inside x's columns")
+    if (n_q_heads, head_dim) != (selector.num_heads, selector.head_dim):
+        raise ValueError("query heads do not match the selector")
+    if check_positions and positions.numel():
+        lo, hi = int(positions.min()), int(positions.max())
+        if lo < 0 or hi >= cos.shape[0]:
+            raise ValueError(f"positions must lie in [0, {cos.shape[0]}) (got {lo}..{hi})")
+    G, n = selector.num_kv_heads, x.shape[0]
+    F = selector.router_heads * selector.router_dim
+    out = torch.empty((G, n, F), dtype=x.dtype, device=dev)
+    hm, _, qp, _ = _masters(selector)
+    L = _hip.lib()
+    dt = _hip.dtype_code(x.dtype)
+    ws = _hip.workspace(L.ls_select_workspace_size(0, 0, 0, n_q_heads, G, head_dim,
+                                                   selector.router_heads, selector.router_dim,
+                                                   0, dt), dev)
+    _hip.check(L.ls_rope_project_queries(
+        x.data_ptr(), x.stride(0), positions.contiguous().data_ptr(), n, n_q_heads, G, head_dim,
+        cos.contiguous().data_ptr(), sin.contiguous().data_ptr(), cos.shape[0], hm.data_ptr(),
+        qp.data_ptr(), selector.router_heads, selector.router_dim, dt, out.data_ptr(),
+        ws.data_ptr(), ws.numel(), _hip.stream_of(dev)), "ls_rope_project_queries")
+    return out
+
+
 def silu_mul(gate_up: torch.Tensor, inter: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """``silu(gate) * up`` for ``gate_up [n, 2*inter]`` = [gate | up] (minicpm.py:1098-1135)."""
     _rows(gate_up, "gate_up")
@@ -344,13 +387,22 @@ class MiniCPMLeanSelect:
         N = h.shape[0]
         qkv = F.linear(h, L.w_qkv)
         cos, sin = self.rope_tables(max(cu_host[i + 1] - cu_host[i] for i in range(len(cu_host) - 1)))
-        # Queries rotate in place; the keys rotate in the pass that also forms
-        # their compressed keys (the attention layer then does not re-read them).
-        fused = cfg.kernel_size == 32 and cfg.kernel_stride == 16
-        rope_inplace(qkv, positions, cos, sin, n_q_heads=H, n_k_heads=0 if fused else G,
-                     k_col_offset=H * D, head_dim=D, check_positions=False)
+        # Producer-side fusion: the queries rotate in the pass that also forms
+        # the selector's query projection, the keys in the pass that also forms
+        # their compressed keys (the selection then re-reads neither).
+        fused_k = cfg.kernel_size == 32 and cfg.kernel_stride == 16
+        F_router = L.selector.router_heads * L.selector.router_dim
+        fused_q = D == 128 and F_router in (64, 128)
+        q_tilde = None
+        if fused_q:
+            q_tilde = rope_project_queries(qkv, positions, cos, sin, L.selector, n_q_heads=H,
+                                           head_dim=D, check_positions=False)
+        if not (fused_q and fused_k):
+            rope_inplace(qkv, positions, cos, sin, n_q_heads=0 if fused_q else H,
+                         n_k_heads=0 if fused_k else G, k_col_offset=H * D, head_dim=D,
+                         check_positions=False)
         compressed = None
-        if fused:
+        if fused_k:
             compressed = rope_k_compress(qkv, positions, cos, sin, cu_seqlens, cu_host,
                                          n_k_heads=G, k_col_offset=H * D, head_dim=D,
                                          check_positions=False)
@@ -363,7 +415,7 @@ class MiniCPMLeanSelect:
             q, k, v, cu_seqlens, L.selector, topk=cfg.topk, local_blocks=cfg.local_blocks,
             init_blocks=cfg.init_blocks, block_size=cfg.block_size, kernel_size=cfg.kernel_size,
             kernel_stride=cfg.kernel_stride, cu_seqlens_host=cu_host, return_topk_idx=True,
-            compressed=compressed)
+            compressed=compressed, q_tilde=q_tilde)
         o = F.linear(attn.view(N, H * D), L.w_o)
         if return_parts:
             return o, dict(qkv=qkv, attn=attn, topk_idx=ids)

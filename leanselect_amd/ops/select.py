@@ -51,12 +51,16 @@ def leanselect_prefill_topk_idx(
     local_blocks: int = 32,
     cache_lens: torch.Tensor | None = None,
     cu_seqlens_q_host: list[int] | None = None,
+    q_tilde: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Page plans ``topk_idx [G, total_q, take]`` int32.
 
     ``q_unpad [total_q, H, D]`` are the post-RoPE queries, ``k_compressed
     [total_atoms, G, D]`` the compressed keys with prefix offsets
     ``cu_seqlens_k`` (int32, device), ``selector`` a ``LeanSelectSelector``.
+    ``q_tilde [G, total_q, R*F]``, when given, is the selector's projection of
+    those queries (as ``rope_project_queries`` forms it while rotating them);
+    the selection then does not read ``q_unpad``.
     """
     if cache_lens is not None:
         raise ValueError("Lightweight selection is prefill only")
@@ -92,6 +96,22 @@ def leanselect_prefill_topk_idx(
         total_q, total_atoms, batch, H, G, D, selector.router_heads, selector.router_dim,
         max_pages, dt)
     ws = _hip.workspace(nbytes, dev)
+    if q_tilde is not None:
+        F = selector.router_heads * selector.router_dim
+        if tuple(q_tilde.shape) != (G, total_q, F) or q_tilde.dtype != q_unpad.dtype \
+                or not q_tilde.is_contiguous() or q_tilde.device != q_unpad.device:
+            raise ValueError(f"q_tilde must be a contiguous [{G}, {total_q}, {F}] "
+                             f"{q_unpad.dtype} tensor on {q_unpad.device}")
+        rc = L.ls_select_prefill_qt(
+            q_tilde.data_ptr(), total_q,
+            k_compressed.data_ptr() if total_atoms else None, k_compressed.stride(0), total_atoms,
+            cu_seqlens_q.contiguous().data_ptr(), cu_seqlens_k.contiguous().data_ptr(), batch,
+            max_seqlen_q, H, G, D, khm.data_ptr(), kp.data_ptr(), selector.router_heads,
+            selector.router_dim, dt, int(topk), block_size, kernel_stride, int(init_blocks),
+            int(local_blocks), topk_idx.data_ptr(), take, ws.data_ptr(), ws.numel(),
+            _hip.stream_of(dev))
+        _hip.check(rc, "ls_select_prefill_qt")
+        return topk_idx
     rc = L.ls_select_prefill(
         q_unpad.data_ptr(), q_unpad.stride(0), total_q,
         k_compressed.data_ptr() if total_atoms else None, k_compressed.stride(0), total_atoms,

@@ -40,13 +40,16 @@ def leanselect_sparse_prefill(
     cu_seqlens_host: list[int] | None = None,
     return_topk_idx: bool = False,
     compressed: tuple[torch.Tensor, torch.Tensor] | None = None,
+    q_tilde: torch.Tensor | None = None,
 ):
     """``(out [total, H, D], topk_idx [G, total, take])`` for packed prefill sequences.
 
     ``topk`` is the total page budget (forced pages included), i.e. the
     reference's ``self.topk = topk + window_size // block_size``.
     ``compressed`` = ``(kc, cu_seqlens_compressed)`` when the producer of ``k``
-    already formed the compressed keys (``minicpm.rope_k_compress``).
+    already formed the compressed keys (``minicpm.rope_k_compress``), and
+    ``q_tilde`` the selector's projection of ``q`` when the producer of ``q``
+    already formed it (``minicpm.rope_project_queries``).
     """
     host = cu_seqlens_host if cu_seqlens_host is not None else cu_seqlens.tolist()
     max_len = max(host[i + 1] - host[i] for i in range(len(host) - 1))
@@ -61,7 +64,7 @@ def leanselect_sparse_prefill(
     ids = leanselect_prefill_topk_idx(
         q, kc, cu_seqlens, cu_c, selector, topk=topk, block_size=block_size,
         kernel_stride=kernel_stride, init_blocks=init_blocks, local_blocks=local_blocks,
-        cu_seqlens_q_host=host)
+        cu_seqlens_q_host=host, q_tilde=q_tilde)
     range_pop()
     range_push("stage 2")
     out = sparse_attention(q, k, v, cu_seqlens, cu_seqlens, max_len, max_len, ids,

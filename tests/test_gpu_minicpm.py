@@ -248,3 +248,48 @@ def test_rope_k_compress_equals_rope_then_compress(dtype):
     assert torch.equal(got, ref)  # keys rotated in place, every other column untouched
     assert torch.equal(cu_c, want_cu)
     assert torch.equal(kc, want_kc)
+
+
+@pytest.mark.parametrize("dtype,router", [(torch.bfloat16, (4, 32)), (torch.float16, (4, 32)),
+                                          (torch.bfloat16, (2, 32))])
+def test_rope_project_queries_equals_rope_then_project(dtype, router):
+    """The fused pass (queries rotated while the selector's projection is formed)
+    gives bit for bit the rotated queries of ls_rope_inplace and the q~ of
+    ls_project_queries on them (router widths 128 and 64), with a row count off
+    the 64-row workgroup grid, the positions of a ragged batch, and every other
+    column untouched."""
+    from leanselect_amd.selector import LeanSelectSelector
+    lens = [1000, 77, 1, 300]
+    N, H, G, D = sum(lens), 32, 2, 128
+    g = torch.Generator(device="cpu").manual_seed(11)
+    x = (torch.randn(N, H * D + 2 * G * D, generator=g) * 2).to(dtype).to(DEV)
+    pos = torch.cat([torch.arange(n, dtype=torch.int32) for n in lens]).to(DEV)
+    cos, sin = minicpm.rotary_tables(D, 2048, 10000.0, DEV)
+    torch.manual_seed(3)
+    sel = LeanSelectSelector(num_heads=H, num_kv_heads=G, head_dim=D, router_heads=router[0],
+                             router_dim=router[1]).to(DEV).requires_grad_(False)
+    ref = x.clone()
+    minicpm.rope_inplace(ref, pos, cos, sin, n_q_heads=H, n_k_heads=0, k_col_offset=H * D)
+    want = sel.project_queries(ref[:, : H * D].view(N, H, D))
+    got = x.clone()
+    qt = minicpm.rope_project_queries(got, pos, cos, sin, sel, n_q_heads=H)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)  # queries rotated in place, key/value columns untouched
+    assert qt.shape == want.shape and torch.equal(qt, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_select_from_q_tilde_equals_select_from_queries(dtype):
+    """ls_select_prefill_qt with the selector's projection of the queries gives
+    the same plans as ls_select_prefill on the queries (ragged batch)."""
+    from leanselect_amd import workloads
+    from leanselect_amd.ops import compress_k, leanselect_prefill_topk_idx
+    case = workloads.hidden_space_layer((3000, 64, 1500), device=DEV, dtype=dtype, seed=4)
+    kc, cu_c = compress_k(case.k, case.cu_seqlens, cu_seqlens_host=case.cu_host)
+    kw = dict(topk=case.topk, init_blocks=case.init_blocks, local_blocks=case.local_blocks,
+              cu_seqlens_q_host=case.cu_host)
+    want = leanselect_prefill_topk_idx(case.q, kc, case.cu_seqlens, cu_c, case.selector, **kw)
+    qt = case.selector.project_queries(case.q)
+    got = leanselect_prefill_topk_idx(case.q, kc, case.cu_seqlens, cu_c, case.selector,
+                                      q_tilde=qt, **kw)
+    assert torch.equal(got, want)
