@@ -238,13 +238,16 @@ __global__ __launch_bounds__(256) void ls_stage1_pool_kernel(
     const float* prow = part + ((int64_t)g * total_q + t) * n_chunks * 32;
     const int nch = (nc + 63) / 64;
     const int h = tid >> 4, share = tid & 15;
+    // (Unrolled so that each thread's partial loads are in flight together.)
     float M = -INFINITY;
     if (h < gs)
+#pragma unroll 8
       for (int c = share; c < nch; c += 16) M = fmaxf(M, prow[c * 32 + 2 * h]);
 #pragma unroll
     for (int o = 8; o >= 1; o >>= 1) M = fmaxf(M, ls_shfl_xor(M, o));
     float L = 0.f;
     if (h < gs && M != -INFINITY)
+#pragma unroll 8
       for (int c = share; c < nch; c += 16) {
         const float mc = prow[c * 32 + 2 * h];
         if (mc != -INFINITY) L += prow[c * 32 + 2 * h + 1] * __builtin_amdgcn_exp2f(mc - M);
@@ -260,6 +263,7 @@ __global__ __launch_bounds__(256) void ls_stage1_pool_kernel(
     float v = -INFINITY;
     if (j >= 0 && j < nc) {
       float s = 0.f;
+#pragma unroll 16
       for (int h = 0; h < gs; ++h) s += __builtin_amdgcn_exp2f(xrow[(int64_t)h * ncpad + j] - s_lse[h]);
       uint16_t o;
       if constexpr (DT == LS_F16)

@@ -840,6 +840,58 @@ __device__ __forceinline__ void ls_topk_row(const void* __restrict__ P, int64_t 
   }
 }
 
+// The end of ls_topk_row16 for n gathered candidates (key << 16 | column,
+// in column order) held in NP slots of the wave's scratch: the kk-th key T
+// bisected from the common bit prefix of lo and the row maximum m1 (per-lane
+// maxima, reduced here), then the chosen columns written in column order.
+template <int NP>
+__device__ __forceinline__ void ls_topk_emit_packed(const uint32_t* __restrict__ scr, int n,
+                                                    uint32_t lo, uint32_t m1, int kk, int lo_end,
+                                                    int lane, int32_t* __restrict__ orow) {
+  uint32_t pk[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) pk[i] = i * 64 + lane < n ? scr[i * 64 + lane] : 0u;
+  uint32_t hi = m1;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, LS_WAVE));
+  hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)hi);
+  // T: the largest 16-bit key with #{key >= T} >= kk, sharing lo's and hi's
+  // common bit prefix.
+  uint32_t T = lo;
+  const uint32_t d = lo ^ hi;
+  if (d != 0u) {
+    const int tb = 31 - __builtin_clz(d);
+    T = lo & ~((2u << tb) - 1u);
+#pragma unroll 1
+    for (int bit = tb; bit >= 0; --bit) {
+      const uint32_t cand = (T | (1u << bit)) << 16;
+      int cnt = 0;
+#pragma unroll
+      for (int i = 0; i < NP; ++i) cnt += __popcll(__ballot(pk[i] >= cand));
+      if (cnt >= kk) T |= 1u << bit;
+    }
+  }
+  const uint32_t above = (T << 16) | 0xffffu;  // packed keys above T
+  int gt = 0;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) gt += __popcll(__ballot(pk[i] > above));
+  const int m = kk - gt;
+  int out_pos = lo_end, eq_before = 0;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const bool valid = i * 64 + lane < n;
+    const bool eq = valid && (pk[i] >> 16) == T;
+    const uint64_t eq_mask = __ballot(eq);
+    const int eq_rank = eq_before + ls_lanes_below(eq_mask);
+    const bool sel = valid && (pk[i] > above || (eq && eq_rank < m));
+    const uint64_t sel_mask = __ballot(sel);
+    const int pos = out_pos + ls_lanes_below(sel_mask);
+    if (sel && pos < lo_end + kk) orow[pos] = lo_end + (int)(pk[i] & 0xffffu);
+    out_pos += __popcll(sel_mask);
+    eq_before += __popcll(eq_mask);
+  }
+}
+
 // The same for 16-bit scores of rows of more than four slots, emitting from
 // the gathered candidates: the keys >= lo (lo = the kk-th largest of the
 // lanes' two largest keys, a lower bound of the kk-th key) are packed as
@@ -901,48 +953,9 @@ __device__ __forceinline__ void ls_topk_row16(const void* __restrict__ P, int64_
     }
     return;
   }
-  uint32_t pk[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) pk[i] = i * 64 + lane < n ? scr[i * 64 + lane] : 0u;
-  uint32_t hi = m1;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, LS_WAVE));
-  hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)hi);
-  // T: the largest 16-bit key with #{key >= T} >= kk, sharing lo's and hi's
-  // common bit prefix.
-  uint32_t T = lo;
-  const uint32_t d = lo ^ hi;
-  if (d != 0u) {
-    const int tb = 31 - __builtin_clz(d);
-    T = lo & ~((2u << tb) - 1u);
-#pragma unroll 1
-    for (int bit = tb; bit >= 0; --bit) {
-      const uint32_t cand = (T | (1u << bit)) << 16;
-      int cnt = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) cnt += __popcll(__ballot(pk[i] >= cand));
-      if (cnt >= kk) T |= 1u << bit;
-    }
-  }
-  const uint32_t above = (T << 16) | 0xffffu;  // packed keys above T
-  int gt = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) gt += __popcll(__ballot(pk[i] > above));
-  const int m = kk - gt;
-  int out_pos = lo_end, eq_before = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const bool valid = i * 64 + lane < n;
-    const bool eq = valid && (pk[i] >> 16) == T;
-    const uint64_t eq_mask = __ballot(eq);
-    const int eq_rank = eq_before + ls_lanes_below(eq_mask);
-    const bool sel = valid && (pk[i] > above || (eq && eq_rank < m));
-    const uint64_t sel_mask = __ballot(sel);
-    const int pos = out_pos + ls_lanes_below(sel_mask);
-    if (sel && pos < lo_end + kk) orow[pos] = lo_end + (int)(pk[i] & 0xffffu);
-    out_pos += __popcll(sel_mask);
-    eq_before += __popcll(eq_mask);
-  }
+  if (n <= 64) return ls_topk_emit_packed<1>(scr, n, lo, m1, kk, lo_end, lane, orow);
+  if (n <= 128) return ls_topk_emit_packed<2>(scr, n, lo, m1, kk, lo_end, lane, orow);
+  return ls_topk_emit_packed<4>(scr, n, lo, m1, kk, lo_end, lane, orow);
 }
 
 template <int KPL, bool KEY32>
@@ -995,10 +1008,26 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
   if (n_slots <= 2) return ls_topk_row<2, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
   if (n_slots <= 4 || KPL <= 4) return ls_topk_row<(KPL < 4 ? KPL : 4), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
   if constexpr (!KEY32) {
-    if (n_slots <= 8 || KPL <= 8) return ls_topk_row16<(KPL < 8 ? KPL : 8)>(P, base, cn, kk, lo_end, lane, orow, scr);
-    if (n_slots <= 16 || KPL <= 16) return ls_topk_row16<(KPL < 16 ? KPL : 16)>(P, base, cn, kk, lo_end, lane, orow, scr);
-    if (n_slots <= 32 || KPL <= 32) return ls_topk_row16<(KPL < 32 ? KPL : 32)>(P, base, cn, kk, lo_end, lane, orow, scr);
-    if (n_slots <= 64 || KPL <= 64) return ls_topk_row16<(KPL < 64 ? KPL : 64)>(P, base, cn, kk, lo_end, lane, orow, scr);
+    // Slot counts in steps of about an eighth, so a row runs few empty slots.
+#define LS_TOPK16_CASE(N)                                                                  \
+  if (n_slots <= (N) || KPL <= (N))                                                        \
+    return ls_topk_row16<(KPL < (N) ? KPL : (N))>(P, base, cn, kk, lo_end, lane, orow, scr);
+    LS_TOPK16_CASE(6)
+    LS_TOPK16_CASE(8)
+    LS_TOPK16_CASE(10)
+    LS_TOPK16_CASE(12)
+    LS_TOPK16_CASE(14)
+    LS_TOPK16_CASE(16)
+    LS_TOPK16_CASE(20)
+    LS_TOPK16_CASE(24)
+    LS_TOPK16_CASE(28)
+    LS_TOPK16_CASE(32)
+    LS_TOPK16_CASE(40)
+    LS_TOPK16_CASE(48)
+    LS_TOPK16_CASE(56)
+    LS_TOPK16_CASE(64)
+    LS_TOPK16_CASE(96)
+#undef LS_TOPK16_CASE
     return ls_topk_row16<KPL>(P, base, cn, kk, lo_end, lane, orow, scr);
   } else {
     if (n_slots <= 8 || KPL <= 8) return ls_topk_row<(KPL < 8 ? KPL : 8), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
