@@ -546,7 +546,11 @@ def model_bench(args, dev) -> None:
             "vocab": cfg.vocab_size, "heads_q": H, "heads_kv": G, "head_dim": D,
             "budget_pages": cfg.topk, "sink_pages": cfg.init_blocks,
             "local_blocks": cfg.local_blocks, "router": f"{cfg.router_heads}x{cfg.router_dim}",
-            "rope": "plain, base 10000", "parallelism": "single-gpu",
+            "rope": ("longrope: MiniCPM4.1 128K factors, base 10000, original context "
+                     f"{cfg.original_max_position_embeddings}, scale "
+                     f"{minicpm.longrope_scale(cfg.max_position_embeddings, cfg.original_max_position_embeddings):.4f}"
+                     if cfg.rope_scaling == "longrope" else "plain, base 10000"),
+            "parallelism": "single-gpu",
         },
         "layer0_stages_ms": ms,
         "layer0_gemm_tflops": round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 1),

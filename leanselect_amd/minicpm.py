@@ -46,6 +46,8 @@ __all__ = [
     "MiniCPMConfig",
     "MiniCPMLeanSelect",
     "rotary_tables",
+    "longrope_scale",
+    "MINICPM41_128K_LONGROPE_FACTOR",
     "rms_layernorm",
     "add_rms_layernorm",
     "rope_inplace",
@@ -64,9 +66,12 @@ class MiniCPMConfig:
     KV heads of 128, FFN 16384, vocabulary 73448) with its published
     ``scale_emb`` 12, ``scale_depth`` 1.4 and ``dim_model_base`` 256 (the
     reference's ``MiniCPMConfig`` defaults are 1, 1, 1:
-    leanselect/models/configuration_minicpm.py:130-132), plain RoPE base 10000,
-    and the LeanSelect geometry of configs/minicpm.json with a 64-page budget
-    (1 sink page, 4 local blocks).
+    leanselect/models/configuration_minicpm.py:130-132), RoPE base 10000 with
+    the LongRoPE scaling the reference installs for MiniCPM4.1 at 128K
+    (``apply_minicpm41_128k_longrope``, leanselect/models/minicpm.py:1011-1023:
+    the published per-frequency factors, original context 65536), and the
+    LeanSelect geometry of configs/minicpm.json with a 64-page budget (1 sink
+    page, 4 local blocks).  ``rope_scaling=None`` gives plain RoPE.
     """
 
     hidden_size: int = 4096
@@ -77,6 +82,9 @@ class MiniCPMConfig:
     vocab_size: int = 73448
     rms_norm_eps: float = 1e-6
     rope_theta: float = 10000.0
+    rope_scaling: str | None = "longrope"
+    max_position_embeddings: int = 65536
+    original_max_position_embeddings: int = 65536
     scale_emb: float = 12.0
     scale_depth: float = 1.4
     dim_model_base: int = 256
@@ -112,13 +120,56 @@ def _out(out: torch.Tensor, shape: tuple, like: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def rotary_tables(head_dim: int, max_pos: int, base: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+# MiniCPM4.1-8B's LongRoPE factors for 128K contexts, one per rotary frequency
+# (the same values serve as short and long factors): the model's published
+# rope_scaling table, as leanselect/models/minicpm.py:942-1008 installs it.
+MINICPM41_128K_LONGROPE_FACTOR = (
+    0.9982316082870437, 1.033048153422584, 1.0749920956484724, 1.1255096879436193,
+    1.1863348602111476, 1.259543828902579, 1.3476188888731149, 1.4535223827776373,
+    1.5807816745852985, 1.7335856049489526, 1.9168922912975785, 2.1365471404135326,
+    2.3994084200118646, 2.713475511863602, 3.0880118452194134, 3.533650295140154,
+    4.062463396503134, 4.687974098908333, 5.425075306704039, 6.289818967956352,
+    7.29902962722721, 8.6357018163639, 10.210822723989212, 12.053807765671676,
+    14.193944598909404, 16.65780676784363, 19.463620727694074, 22.628311203524586,
+    26.150106147261315, 30.02526691405111, 34.23183327975347, 38.73811934094828,
+    43.502489489729555, 48.47627117965394, 53.61139491762471, 58.857366522037935,
+    64.16798299215064, 69.51359464319125, 74.86555458220285, 80.21497790341579,
+    85.55322183307433, 90.89611806932027, 96.26245306514224, 101.68269304046481,
+    107.18619510219668, 112.82253283014026, 118.63764063163615, 119.88866203644656,
+    120.9462882391725, 121.837565139014, 122.58663780572562, 123.2147719894291,
+    123.74049454862576, 124.17980424685767, 124.54641761955492, 124.85202548028222,
+    125.10654406389756, 125.31835105170659, 125.49450117164764, 125.64091910903052,
+    125.76256945356558, 125.86360463815589, 125.94749252260765, 126.01712561287873,
+)
+
+
+def longrope_scale(max_position_embeddings: int, original_max_position_embeddings: int) -> float:
+    """``MiniCPMLongRoPE``'s cos/sin scale (minicpm.py:908-914):
+    sqrt(1 + log(max / original) / log(original))."""
+    s = max_position_embeddings / original_max_position_embeddings
+    return math.sqrt(1 + math.log(s) / math.log(original_max_position_embeddings))
+
+
+def rotary_tables(head_dim: int, max_pos: int, base: float, device, *,
+                  ext_factors=None, scale: float = 1.0) -> tuple[torch.Tensor, torch.Tensor]:
     """float32 ``(cos, sin)`` ``[max_pos, head_dim]`` built like
-    ``MiniCPMRotaryEmbedding._set_cos_sin_cache`` (minicpm.py:804-838)."""
+    ``MiniCPMRotaryEmbedding._set_cos_sin_cache`` (minicpm.py:804-838), or, with
+    ``ext_factors`` (one per frequency), like ``MiniCPMLongRoPE._set_cos_sin_cache``
+    (minicpm.py:917-939): ``freqs = outer(t, 1 / ext_factors) * inv_freq`` and both
+    tables multiplied by ``scale``."""
     inv_freq = 1.0 / base ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim)
     t = torch.arange(max_pos, device=device, dtype=inv_freq.dtype)
-    emb = torch.cat((torch.outer(t, inv_freq),) * 2, dim=-1)
-    return emb.cos().contiguous(), emb.sin().contiguous()
+    if ext_factors is None:
+        freqs = torch.outer(t, inv_freq)
+    else:
+        ext = torch.tensor(ext_factors, dtype=torch.float32, device=device)
+        if ext.shape != inv_freq.shape:
+            raise ValueError(f"need {inv_freq.numel()} LongRoPE factors, got {ext.numel()}")
+        freqs = torch.mul(torch.outer(t, 1.0 / ext), inv_freq)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    if ext_factors is None:
+        return emb.cos().contiguous(), emb.sin().contiguous()
+    return (emb.cos() * scale).contiguous(), (emb.sin() * scale).contiguous()
 
 
 def rms_layernorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
@@ -365,7 +416,17 @@ class MiniCPMLeanSelect:
         not depend on the table length)."""
         if self._rope is None or self._rope[0].shape[0] < max_pos:
             n = max(max_pos, 2 * self._rope[0].shape[0]) if self._rope is not None else max_pos
-            self._rope = rotary_tables(self.cfg.head_dim, n, self.cfg.rope_theta, self.device)
+            cfg = self.cfg
+            if cfg.rope_scaling == "longrope":
+                self._rope = rotary_tables(
+                    cfg.head_dim, n, cfg.rope_theta, self.device,
+                    ext_factors=MINICPM41_128K_LONGROPE_FACTOR,
+                    scale=longrope_scale(cfg.max_position_embeddings,
+                                         cfg.original_max_position_embeddings))
+            elif cfg.rope_scaling is None:
+                self._rope = rotary_tables(cfg.head_dim, n, cfg.rope_theta, self.device)
+            else:
+                raise ValueError(f"unsupported rope_scaling {cfg.rope_scaling!r}")
         return self._rope
 
     @property

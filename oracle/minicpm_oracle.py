@@ -14,6 +14,7 @@ import torch
 
 __all__ = [
     "rotary_tables",
+    "longrope_scale",
     "rms_layernorm",
     "apply_rotary_pos_emb",
     "silu_mul",
@@ -22,18 +23,33 @@ __all__ = [
 ]
 
 
-def rotary_tables(head_dim: int, max_pos: int, base: float = 10000.0):
+def rotary_tables(head_dim: int, max_pos: int, base: float = 10000.0, ext_factors=None,
+                  scale: float = 1.0):
     """``(cos, sin)`` float32 ``[max_pos, head_dim]``.
 
     ``MiniCPMRotaryEmbedding._set_cos_sin_cache`` (minicpm.py:804-838):
     ``inv_freq = 1 / base ** (arange(0, dim, 2) / dim)``, ``freqs = outer(t,
     inv_freq)``, ``emb = cat(freqs, freqs)``, then ``cos``/``sin`` in float32.
+    With ``ext_factors``, ``MiniCPMLongRoPE._set_cos_sin_cache`` (minicpm.py:917-939):
+    ``freqs = outer(t, 1 / ext_factors) * inv_freq`` and ``cos``/``sin`` times ``scale``
+    (``longrope_scale``).
     """
     inv_freq = 1.0 / base ** (torch.arange(0, head_dim, 2).float() / head_dim)
     t = torch.arange(max_pos, dtype=inv_freq.dtype)
-    freqs = torch.outer(t, inv_freq)
+    if ext_factors is None:
+        freqs = torch.outer(t, inv_freq)
+        emb = torch.cat((freqs, freqs), dim=-1)
+        return emb.cos().to(torch.float32), emb.sin().to(torch.float32)
+    ext = torch.tensor(ext_factors, dtype=torch.float32)
+    freqs = torch.mul(torch.outer(t, 1.0 / ext), inv_freq.to(torch.float32))
     emb = torch.cat((freqs, freqs), dim=-1)
-    return emb.cos().to(torch.float32), emb.sin().to(torch.float32)
+    return emb.cos().to(torch.float32) * scale, emb.sin().to(torch.float32) * scale
+
+
+def longrope_scale(max_position_embeddings: int, original_max_position_embeddings: int) -> float:
+    """``MiniCPMLongRoPE.__init__``'s ``scaling_factor`` (minicpm.py:908-914)."""
+    s = max_position_embeddings / original_max_position_embeddings
+    return math.sqrt(1 + math.log(s) / math.log(original_max_position_embeddings))
 
 
 def rms_layernorm(hidden: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:

@@ -174,3 +174,57 @@ def test_model_wrappers_check_outputs_and_views_before_any_launch(monkeypatch):
     with pytest.raises(ValueError, match="inside"):
         minicpm.rope_inplace(qkv[:, :4096], torch.zeros(4, dtype=torch.int32), cos, cos,
                              n_q_heads=32, n_k_heads=2, k_col_offset=4096)
+
+
+def test_longrope_tables_closed_form():
+    """LongRoPE tables (MiniCPMLongRoPE, minicpm.py:895-939) against float64:
+    angle t / f_i * base^(-2i/D), both tables times the scale; t = 0 gives
+    (scale, 0); unit factors and unit scale give the plain tables bit for bit."""
+    from leanselect_amd.minicpm import MINICPM41_128K_LONGROPE_FACTOR as FAC
+    D, P, base = 128, 3000, 10000.0
+    sc = oracle.longrope_scale(131072, 65536)
+    cos, sin = oracle.rotary_tables(D, P, base, ext_factors=FAC, scale=sc)
+    i = torch.arange(D // 2, dtype=torch.float64)
+    f = torch.tensor(FAC, dtype=torch.float64)
+    theta = torch.arange(P, dtype=torch.float64)[:, None] / f[None, :] * base ** (-2 * i / D)[None, :]
+    tol = 8 * torch.finfo(torch.float32).eps * (1 + theta) * sc
+    for half in (slice(0, D // 2), slice(D // 2, D)):
+        assert bool(((cos[:, half].double() - sc * theta.cos()).abs() <= tol).all())
+        assert bool(((sin[:, half].double() - sc * theta.sin()).abs() <= tol).all())
+    assert torch.allclose(cos[0].double(), torch.full((D,), sc, dtype=torch.float64), rtol=0, atol=1e-7)
+    assert torch.equal(sin[0], torch.zeros(D))
+    c1, s1 = oracle.rotary_tables(D, 500, base, ext_factors=[1.0] * (D // 2), scale=1.0)
+    c0, s0 = oracle.rotary_tables(D, 500, base)
+    assert torch.equal(c1, c0) and torch.equal(s1, s0)
+    # A planted mistake (factor multiplied instead of divided) must fail the bound.
+    bad = torch.cat([(torch.arange(P, dtype=torch.float64)[:, None] * f[None, :]
+                      * base ** (-2 * i / D)[None, :]).cos() * sc] * 2, dim=-1)
+    assert not bool(((bad - sc * torch.cat([theta.cos()] * 2, dim=-1)).abs() <= torch.cat([tol] * 2, dim=-1)).all())
+
+
+def test_longrope_scale_and_factor_table():
+    """sqrt(1 + log(s) / log(L)) at s = 1, 2 and 4 (L = 65536 = 2^16: 1, sqrt(17/16),
+    sqrt(18/16)); the factor table holds 64 increasing values from 0.998 to 126.02
+    (its sum pins every entry to the published table's)."""
+    from leanselect_amd import minicpm
+    assert minicpm.longrope_scale(65536, 65536) == 1.0
+    assert math.isclose(minicpm.longrope_scale(131072, 65536), math.sqrt(17 / 16), rel_tol=1e-15)
+    assert math.isclose(oracle.longrope_scale(262144, 65536), math.sqrt(18 / 16), rel_tol=1e-15)
+    fac = minicpm.MINICPM41_128K_LONGROPE_FACTOR
+    assert len(fac) == 64 and all(b > a for a, b in zip(fac, fac[1:]))
+    assert math.isclose(fac[0], 0.9982316082870437) and math.isclose(fac[-1], 126.01712561287873)
+    assert math.isclose(sum(fac), 3606.5291185034357, rel_tol=1e-15)
+
+
+def test_model_longrope_tables_equal_the_oracle_on_cpu():
+    """The model's table builder (torch on any device) run on the CPU equals the
+    oracle's restatement bit for bit, LongRoPE and plain."""
+    from leanselect_amd import minicpm
+    fac = minicpm.MINICPM41_128K_LONGROPE_FACTOR
+    sc = minicpm.longrope_scale(65536, 65536)
+    c, s = minicpm.rotary_tables(128, 2000, 10000.0, "cpu", ext_factors=fac, scale=sc)
+    co, so = oracle.rotary_tables(128, 2000, 10000.0, ext_factors=fac, scale=sc)
+    assert torch.equal(c, co) and torch.equal(s, so)
+    c, s = minicpm.rotary_tables(128, 2000, 10000.0, "cpu")
+    co, so = oracle.rotary_tables(128, 2000, 10000.0)
+    assert torch.equal(c, co) and torch.equal(s, so)
