@@ -197,3 +197,48 @@ def test_attention_spin_limit_hook_is_host_only():
     assert lib.ls_attn_set_spin_limit(5) == default
     assert lib.ls_attn_set_spin_limit(-1) == 5
     assert lib.ls_attn_set_spin_limit(-1) == default
+
+
+def test_fused_query_and_decode_entry_points_validate_before_any_launch():
+    """The fused rotation + q~ projection, selection from a given q~ and the decode
+    entry points reject unsupported geometry with an error code and message,
+    without a GPU."""
+    lib = _hip.lib()
+    B = _hip.LS_BF16
+    # ls_rope_project_queries: fp32 queries, head_dim 64, router width 96, bad stride.
+    args = [None, 4096, None, 10, 32, 2, 128, None, None, 100, None, None, 4, 32]
+    rc = lib.ls_rope_project_queries(*args, _hip.LS_F32, None, None, 0, None)
+    assert rc == _hip.LS_ERR_UNSUPPORTED and b"bf16 or fp16" in lib.ls_last_error()
+    rc = lib.ls_rope_project_queries(None, 4096, None, 10, 32, 2, 64, None, None, 100, None,
+                                     None, 4, 32, B, None, None, 0, None)
+    assert rc == _hip.LS_ERR_UNSUPPORTED and b"head_dim 128" in lib.ls_last_error()
+    rc = lib.ls_rope_project_queries(None, 4096, None, 10, 32, 2, 128, None, None, 100, None,
+                                     None, 3, 32, B, None, None, 0, None)
+    assert rc == _hip.LS_ERR_UNSUPPORTED and b"router width" in lib.ls_last_error()
+    rc = lib.ls_rope_project_queries(None, 4000, None, 10, 32, 2, 128, None, None, 100, None,
+                                     None, 4, 32, B, None, None, 0, None)
+    assert rc == _hip.LS_ERR_INVALID and b"stride" in lib.ls_last_error()
+    rc = lib.ls_rope_project_queries(None, 4096, None, 10, 32, 2, 128, None, None, 100, None,
+                                     None, 4, 32, B, None, None, 0, None)
+    assert rc == _hip.LS_ERR_INVALID and b"null" in lib.ls_last_error()
+    # ls_select_prefill_qt: take must be min(topk, pages) and q_tilde non-null.
+    rc = lib.ls_select_prefill_qt(None, 10, None, 0, 0, None, None, 1, 10, 32, 2, 128, None,
+                                  None, 4, 32, B, 64, 64, 16, 1, 4, None, 5, None, 0, None)
+    assert rc == _hip.LS_ERR_INVALID and b"ls_select_prefill_qt" in lib.ls_last_error()
+    rc = lib.ls_select_prefill_qt(None, 10, None, 0, 0, None, None, 1, 10, 32, 2, 128, None,
+                                  None, 4, 32, B, 64, 64, 16, 1, 4, None, 1, None, 0, None)
+    assert rc == _hip.LS_ERR_INVALID and b"null" in lib.ls_last_error()
+    # ls_decode_select: out_len beyond the LDS key buffer, take above out_len.
+    rc = lib.ls_decode_select(None, 4096, None, 1, None, 0, 256, None, 1, 10, 32, 2, 128, B,
+                              0.088, 64, 64, 32, 16, 1, 4, 40000, 64, None, None, 0, None)
+    assert rc == _hip.LS_ERR_UNSUPPORTED and b"pages per row" in lib.ls_last_error()
+    rc = lib.ls_decode_select(None, 4096, None, 1, None, 0, 256, None, 1, 10, 32, 2, 128, B,
+                              0.088, 64, 64, 32, 16, 1, 4, 10, 64, None, None, 0, None)
+    assert rc == _hip.LS_ERR_INVALID and b"take" in lib.ls_last_error()
+    # ls_sparse_attn_kvcache: more than 256 plan ids per row, too many splits.
+    rc = lib.ls_sparse_attn_kvcache(None, 4096, None, 1, None, None, 0, 256, None, 1, 32, 2,
+                                    128, B, None, 300, 0.088, 0, 4, None, None, None, 0, None)
+    assert rc == _hip.LS_ERR_UNSUPPORTED and b"plan ids" in lib.ls_last_error()
+    rc = lib.ls_sparse_attn_kvcache(None, 4096, None, 1, None, None, 0, 256, None, 1, 32, 2,
+                                    128, B, None, 64, 0.088, 0, 65, None, None, None, 0, None)
+    assert rc == _hip.LS_ERR_INVALID and b"n_splits" in lib.ls_last_error()
