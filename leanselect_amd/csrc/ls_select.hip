@@ -898,8 +898,8 @@ __device__ __forceinline__ void ls_topk_emit_packed(const uint32_t* __restrict__
 // key << 16 | column into at most four slots in column order, the kk-th key T
 // is bisected on them from the common bit prefix of lo and the row maximum,
 // and the chosen columns (keys > T, then the lowest-column ties) are written
-// from those four slots instead of from all NS.  When the packed set would
-// overflow its 256 entries the row takes ls_topk_row.
+// from those four slots instead of from all NS.  When more than 256 keys pass
+// (or no bound exists) the row is searched and emitted over all NS slots.
 template <int NS>
 __device__ __forceinline__ void ls_topk_row16(const void* __restrict__ P, int64_t base, int cn,
                                               int kk, int lo_end, int lane,
@@ -907,30 +907,51 @@ __device__ __forceinline__ void ls_topk_row16(const void* __restrict__ P, int64_
                                               uint32_t* __restrict__ scr) {
   if (NS <= 4 || kk < 1 || kk > 128)
     return ls_topk_row<NS, false>(P, base, cn, kk, lo_end, lane, orow, scr);
+  // Keys are held shifted up by 16 (order key << 16), so a gathered entry is
+  // key | column; 0 marks a column past the row.  Only the slots that reach
+  // the row's end (a uniform test) pay for the per-lane column check.
+  cn = __builtin_amdgcn_readfirstlane(cn);
   uint32_t key[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) key[s] = ((const uint16_t*)P)[base + min(s * 64 + lane, cn - 1)];
+  const int n_full = cn >> 6;  // slots lying wholly inside the row (uniform)
   uint32_t m1 = 0u, m2 = 0u;
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    key[s] = s * 64 + lane < cn ? ls_order_key16((uint16_t)key[s]) : 0u;
-    m2 = max(m2, min(m1, key[s]));
-    m1 = max(m1, key[s]);
+    const uint32_t b = key[s];
+    uint32_t k = (b ^ ((b >> 15) * 0x7fffu) ^ 0x8000u) << 16;  // ls_order_key16(b) << 16
+    if (s >= n_full) k = s * 64 + lane < cn ? k : 0u;
+    key[s] = k;
+    m2 = max(m2, min(m1, k));
+    m1 = max(m1, k);
   }
+  m1 >>= 16;
+  m2 >>= 16;
   const uint32_t mm[2] = {m1, m2};
   const uint32_t lo = ls_kth_bisect<2>(mm, kk, 0u, 15);
+  // Gather the keys >= lo with their columns, in column order; stop once more
+  // than 256 have been found (the scratch holds 256 + 63).
   int n = 0;
   if (lo != 0u) {
+    const uint32_t lo_sh = lo << 16;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const bool sv = key[s] >= lo;
-      const uint64_t mk = __ballot(sv);
-      const int pos = n + ls_lanes_below(mk);
-      if (sv && pos < 256) scr[pos] = (key[s] << 16) | (uint32_t)(s * 64 + lane);
-      n += __popcll(mk);
+      if (n <= 256) {
+        const bool sv = key[s] >= lo_sh;
+        const uint64_t mk = __ballot(sv);
+        const int pos = (int)__builtin_amdgcn_mbcnt_hi(
+            (uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, (uint32_t)n));
+        if (sv) scr[pos] = key[s] | (uint32_t)(s * 64 + lane);
+        n += __popcll(mk);
+      }
     }
   }
   if (lo == 0u || n > 256) {  // no usable bound: every slot is searched and emitted
+#pragma unroll
+    for (int s = 0; s < NS; ++s) key[s] >>= 16;
+    // (The row length is re-read through an empty asm so that the column
+    // checks below are formed here, not kept alive from the loop above.)
+    asm volatile("" : "+s"(cn));
     const uint32_t T = ls_kth_bisect<NS>(key, kk, 0u, 15);
     int gt = 0;
 #pragma unroll
@@ -963,7 +984,7 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
     const void* __restrict__ P, int64_t p_stride, const int32_t* __restrict__ cu_q,
     const int32_t* __restrict__ cu_a, int batch, int64_t total_q, int G, int take,
     int init_blocks, int local_blocks, int block_size, int32_t* __restrict__ topk_idx) {
-  __shared__ uint32_t s_scr[4][256];  // per-wave gather space of the k-th key search
+  __shared__ uint32_t s_scr[4][320];  // per-wave gather space of the k-th key search
   const int lane = threadIdx.x & 63;
   // The wave index is uniform: keep the row and everything derived from it scalar.
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
