@@ -256,6 +256,66 @@ __device__ __forceinline__ void ls_mark_topk(const uint32_t (&key)[NS], uint32_t
   }
 }
 
+// Stage 1 from n gathered entries key << 16 | page (page order) held in NP
+// slots of the wave's scratch: the kk-th key T bisected from the common bit
+// prefix of lo and the row maximum (per-lane maxima m1, reduced here), then the
+// kk chosen pages (key > T, then the lowest pages with key == T) set in the
+// scratch, cleared first to an n_words page bitmap.  Returns |S|.
+template <int NP>
+__device__ __forceinline__ int ls_nosa_mark_packed(uint32_t* __restrict__ scr, int n, uint32_t lo,
+                                                   uint32_t m1, int kk, int n_words, int lane) {
+  uint32_t pk[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) pk[i] = i * 64 + lane < n ? scr[i * 64 + lane] : 0u;
+  uint32_t hi = m1;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, LS_WAVE));
+  hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)hi);
+  uint32_t T = lo;
+  const uint32_t d = lo ^ hi;
+  if (d != 0u) {
+    const int tb = 31 - __builtin_clz(d);
+    T = lo & ~((2u << tb) - 1u);
+#pragma unroll 1
+    for (int bit = tb; bit >= 0; --bit) {
+      const uint32_t cand = (T | (1u << bit)) << 16;
+      int cnt = 0;
+#pragma unroll
+      for (int i = 0; i < NP; ++i) cnt += __popcll(__ballot(pk[i] >= cand));
+      if (cnt >= kk) T |= 1u << bit;
+    }
+  }
+  const uint32_t above = (T << 16) | 0xffffu;  // packed entries above T
+  int gt = 0;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) gt += __popcll(__ballot(pk[i] > above));
+  const int m = kk - gt;
+  // Every lane has read its entries: the scratch becomes the bitmap.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (int i = lane; i < n_words; i += 64) scr[i] = 0u;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int n_sel = 0, eq_before = 0;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const bool valid = i * 64 + lane < n;
+    const bool eq = valid && (pk[i] >> 16) == T;
+    const uint64_t eq_mask = __ballot(eq);
+    const int eq_rank = eq_before + ls_lanes_below(eq_mask);
+    const bool sel = valid && (pk[i] > above || (eq && eq_rank < m));
+    if (sel) {
+      const uint32_t page = pk[i] & 0xffffu;
+      atomicOr(&scr[page >> 5], 1u << (page & 31));
+    }
+    n_sel += __popcll(__ballot(sel));
+    eq_before += __popcll(eq_mask);
+  }
+  return n_sel;
+}
+
 // Key widths: stage 1 uses 16-bit keys for 16-bit page scores (KEY32 off);
 // stage 2 uses the top 16 bits of the float32 keys when the CIS page scores
 // are bf16 values (CIS32 off: their low 16 bits are zero), so each bisection
@@ -292,25 +352,60 @@ __device__ __forceinline__ void ls_nosa_topk_row(
     else k = ninf1;
     key[s] = k;
   }
-  uint32_t shortlist[NW];
-#pragma unroll
-  for (int i = 0; i < NW; ++i) shortlist[i] = 0u;
-  ls_mark_topk<NS>(key, ls_kth_key_row<NS, KEY32 ? 32 : 16>(key, qk_select, scr, lane), qk_select,
-                   shortlist);
-  // Stage 2.  The wave's scratch (free once stage 1 is done) becomes the
-  // chosen-page bitmap: S first, then the block order's first take - |S|
-  // pages outside S.
+  // Stage 1 ends with the shortlist S as a page bitmap in the wave's scratch
+  // (n_s = |S|); stage 2 then adds the block order's first take - |S| pages
+  // outside S to it.
   const int n_words = (out_len + 31) >> 5;
-  for (int i = lane; i < n_words; i += 64) scr[i] = 0u;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  int n_s = 0;
+  int n_s = -1;
+  if constexpr (!KEY32 && NS > 4) {
+    // Long rows: the keys >= lo (lo = the qk_select-th largest of the lanes'
+    // two largest keys) are gathered as key << 16 | page in page order, and S
+    // is marked from them (ls_nosa_mark_packed); otherwise the generic path.
+    if (qk_select >= 1 && qk_select <= 128) {
+      uint32_t m1 = 0u, m2 = 0u;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const uint64_t m = __ballot((shortlist[s >> 5] >> (s & 31)) & 1u);
-    if (lane < 2) scr[2 * s + lane] = lane ? (uint32_t)(m >> 32) : (uint32_t)m;
-    n_s += __popcll(m);
+      for (int s = 0; s < NS; ++s) {
+        m2 = max(m2, min(m1, key[s]));
+        m1 = max(m1, key[s]);
+      }
+      const uint32_t mm[2] = {m1, m2};
+      const uint32_t lo = ls_kth_bisect<2>(mm, qk_select, 0u, 15);
+      int n = 0;
+      if (lo != 0u) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          if (n <= 256) {
+            const bool sv = key[s] >= lo;
+            const uint64_t mk = __ballot(sv);
+            const int pos = (int)__builtin_amdgcn_mbcnt_hi(
+                (uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, (uint32_t)n));
+            if (sv) scr[pos] = (key[s] << 16) | (uint32_t)(s * 64 + lane);
+            n += __popcll(mk);
+          }
+        }
+        if (n <= 64) n_s = ls_nosa_mark_packed<1>(scr, n, lo, m1, qk_select, n_words, lane);
+        else if (n <= 128) n_s = ls_nosa_mark_packed<2>(scr, n, lo, m1, qk_select, n_words, lane);
+        else if (n <= 256) n_s = ls_nosa_mark_packed<4>(scr, n, lo, m1, qk_select, n_words, lane);
+      }
+    }
+  }
+  if (n_s < 0) {
+    uint32_t shortlist[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) shortlist[i] = 0u;
+    ls_mark_topk<NS>(key, ls_kth_key_row<NS, KEY32 ? 32 : 16>(key, qk_select, scr, lane),
+                     qk_select, shortlist);
+    for (int i = lane; i < n_words; i += 64) scr[i] = 0u;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    n_s = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const uint64_t m = __ballot((shortlist[s >> 5] >> (s & 31)) & 1u);
+      if (lane < 2) scr[2 * s + lane] = lane ? (uint32_t)(m >> 32) : (uint32_t)m;
+      n_s += __popcll(m);
+    }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -494,7 +589,7 @@ __global__ __launch_bounds__(256) void ls_nosa_topk_kernel(
     int64_t total_q, int G, int max_seqlen_q, int out_len, int init_blocks, int local_blocks,
     int qk_select, int take, int block_size, uint32_t pinf1, uint32_t ninf1,
     const int32_t* __restrict__ order, int64_t n_blk, int n_order, int32_t* __restrict__ topk_idx) {
-  __shared__ uint32_t s_scr[4][256];  // per-wave k-th key scratch, then the chosen-page bitmap
+  __shared__ uint32_t s_scr[4][320];  // per-wave k-th key scratch, then the chosen-page bitmap
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t n_rows = (int64_t)G * total_q;
