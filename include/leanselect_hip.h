@@ -508,7 +508,7 @@ int ls_kvcache_append(void* k_cache, void* v_cache, int64_t cache_batch_stride,
  * (ties to the lower page), ascending, ids past the row's own page replaced
  * by -1.  topk_idx: int32 [G, total_q, take].  max_kc = n_c of the longest
  * sequence; out_len = ceil((max len_q + max(len - len_q)) / block_size)
- * (at most 32768).  head_dim 128, at most 16 query heads per KV head; kc_cache rows
+ * (at most 30720).  head_dim 128, at most 16 query heads per KV head; kc_cache rows
  * dense (kc_row_stride = G * D).  Workspace from
  * ls_decode_select_workspace_size.
  * Replaces compressed_attention with cache_lens (leanselect/models/minicpm.py:594-705,

@@ -303,7 +303,7 @@ __global__ __launch_bounds__(256) void ls_stage1_pool_kernel(
 // lowest-page m = take - #{key > T} pages with key == T are compacted in page
 // order (thread i owns a contiguous run of pages).
 // ---------------------------------------------------------------------------
-#define LS_DEC_TOPK_MAX_PAGES 32768  // LDS keys (64 KB)
+#define LS_DEC_TOPK_MAX_PAGES 30720  // LDS keys (60 KB, with the static arrays under 64 KB)
 
 __global__ __launch_bounds__(256) void ls_decode_topk_kernel(
     const uint16_t* __restrict__ pooled, const int32_t* __restrict__ cu_q, int batch,
