@@ -530,18 +530,23 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_mfma_kernel(
       for (int ks = 0; ks < KS; ++ks) acc[tb] = LsElem<DT>::mfma(kc[ks], qf[tb][ks], acc[tb]);
     }
     const int atom0 = 16 * j + 4 * q;
-    const bool tail = 16 * j + 15 >= n_at;  // uniform: only the last step has atoms past the end
+    if (16 * j + 15 >= n_at) {  // uniform: only the last step has atoms past the end
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      if (tail) {
+      for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           if (atom0 + i >= n_at) acc[tb][i] = -INFINITY;
-      }
+    }
+    // Atom 4q - 1 of each page comes from the lane group below; the four
+    // cross-lane reads are issued together, so their latencies overlap.
+    float rot[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) rot[tb] = ls_shfl(acc[tb][3], (lane - 16) & 63);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
       const float m4 = fmaxf(fmaxf(acc[tb][0], acc[tb][1]), fmaxf(acc[tb][2], acc[tb][3]));
-      const float rot = ls_shfl(acc[tb][3], (lane - 16) & 63);
-      const float prev = q == 0 ? carry[tb] : rot;
-      carry[tb] = rot;
+      const float prev = q == 0 ? carry[tb] : rot[tb];
+      carry[tb] = rot[tb];
       so[(16 * tb + r) * SP + 4 * (j & 15) + q] = LsElem<DT>::from_f(fmaxf(m4, prev));
     }
     if ((j & 15) == 15 || j == jw_hi) flush(j >> 4);
@@ -659,11 +664,16 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_panel_kernel(
     const int pc = lane & 15, pp = pg0 + 4 * pc;
     const bool full = wide && pp >= fa && pp + 3 <= fb;
     const bool part = !full && pp <= fb && pp + 3 >= fa;
-#pragma unroll 4
+    // All sixteen staged pieces are read first, so their LDS latencies overlap.
+    uint2 vs[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it)
+      vs[it] = *reinterpret_cast<const uint2*>(so + (4 * it + (lane >> 4)) * SP + 4 * pc);
+#pragma unroll
     for (int it = 0; it < 16; ++it) {
       const int tk = 4 * it + (lane >> 4);
       if (tq0 + tk >= tq_end || !(full || part)) continue;
-      const uint2 v = *reinterpret_cast<const uint2*>(so + tk * SP + 4 * pc);
+      const uint2 v = vs[it];
       uint16_t* dst = out + ((int64_t)g * Nq + tq0 + tk) * out_stride + pp;
       if (full) {
         *reinterpret_cast<uint2*>(dst) = v;
@@ -694,11 +704,12 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_panel_kernel(
   };
 
   float carry[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  auto step = [&](int j, const uint8_t* kb) {
-    ls_u32x4 kf[KS];
+  auto read_k = [&](ls_u32x4 (&kf)[KS], const uint8_t* kb) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       kf[ks] = *reinterpret_cast<const ls_u32x4*>(kb + r * ROWB + 16 * ((4 * ks + q) ^ r));
+  };
+  auto step = [&](int j, const ls_u32x4 (&kf)[KS]) {
     ls_f32x4 acc[4];
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
@@ -707,36 +718,51 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_panel_kernel(
       for (int ks = 0; ks < KS; ++ks) acc[tb] = LsElem<DT>::mfma(kf[ks], qf[tb][ks], acc[tb]);
     }
     const int atom0 = 16 * j + 4 * q;
-    const bool tail = 16 * j + 15 >= n_at;  // uniform: only the last step has atoms past the end
+    if (16 * j + 15 >= n_at) {  // uniform: only the last step has atoms past the end
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      if (tail) {
+      for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           if (atom0 + i >= n_at) acc[tb][i] = -INFINITY;
-      }
+    }
+    // Atom 4q - 1 of each page comes from the lane group below; the four
+    // cross-lane reads are issued together, so their latencies overlap.
+    float rot[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) rot[tb] = ls_shfl(acc[tb][3], (lane - 16) & 63);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
       const float m4 = fmaxf(fmaxf(acc[tb][0], acc[tb][1]), fmaxf(acc[tb][2], acc[tb][3]));
-      const float rot = ls_shfl(acc[tb][3], (lane - 16) & 63);
-      const float prev = q == 0 ? carry[tb] : rot;
-      carry[tb] = rot;
+      const float prev = q == 0 ? carry[tb] : rot[tb];
+      carry[tb] = rot[tb];
       so[(16 * tb + r) * SP + 4 * (j & 15) + q] = LsElem<DT>::from_f(fmaxf(m4, prev));
     }
-    if ((j & 15) == 15 || j == jw_hi) flush(j >> 4);
   };
 
-  stage(j_first, 0);
+  // Batches start at multiples of NSTEP, so a 64-page block (16 steps) always
+  // ends on a batch's last step and is written out after it.
+  const int jb0 = j_first & ~(NSTEP - 1);
+  stage(jb0, 0);
   int buf = 0;
-  for (int jb = j_first; jb <= j_hi; jb += NSTEP, buf ^= 1) {
+  for (int jb = jb0; jb <= j_hi; jb += NSTEP, buf ^= 1) {
     // This batch has landed (every wave waited for its own loads), and every
     // wave is done with the other buffer, which the next batch may overwrite.
     LS_WAIT_VMCNT(0);
     __syncthreads();
     if (jb + NSTEP <= j_hi) stage(jb + NSTEP, buf ^ 1);
+    // Each step's k~ fragments are read from LDS while the step before it
+    // computes (two fragment sets used in turn).
+    ls_u32x4 kf[2][KS];
+    read_k(kf[0], &s_k[buf][0]);
 #pragma unroll
     for (int st = 0; st < NSTEP; ++st) {
       const int j = jb + st;
-      if (j <= jw_hi) step(j, &s_k[buf][st * STEPB]);
+      if (st + 1 < NSTEP) read_k(kf[(st + 1) & 1], &s_k[buf][(st + 1) * STEPB]);
+      if (j >= j_first && j <= jw_hi) step(j, kf[st & 1]);
     }
+    // The wave's last step, or a block's last step, was in this batch.
+    const int jl = min(jb + NSTEP - 1, jw_hi);
+    if (jl >= jb && jl >= j_first && ((jl & 15) == 15 || jl == jw_hi)) flush(jl >> 4);
   }
 }
 
