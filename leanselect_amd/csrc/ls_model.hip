@@ -8,6 +8,8 @@
 // Every product and sum rounds separately, as in the reference's torch
 // expressions: this file is built with -ffp-contract=off (no fused
 // multiply-adds).
+#include <type_traits>
+
 #include "ls_common.h"
 
 namespace {
@@ -43,52 +45,63 @@ __device__ __forceinline__ float ls_round(float x) {
 //   out = round(float(n) * float(w)).
 // With ADD, the row is first the new residual (minicpm.py:3616-3625):
 //   x = round(float(res) + float(round(float(h) * c)))   (written back to res).
-// A lane holds 8-element chunks lane*8 + 512*i of the row in registers.
+// A lane holds 8-element chunks lane*8 + 512*i of the row in registers, NC of
+// them (the row's chunk count over 64, rounded up to a power of two).  All of
+// a row's loads are issued before any is used (indices past the row are
+// clamped into it and their values not used), so their latencies overlap.
 // ---------------------------------------------------------------------------
 #define LS_NORM_MAX_CHUNKS 16  // hidden <= 64 lanes * 8 * 16 = 8192
 
-template <int DT, bool ADD>
+template <int DT, bool ADD, int NC>
 __global__ __launch_bounds__(256) void ls_rmsnorm_kernel(
     uint16_t* __restrict__ x, int64_t xs, const uint16_t* __restrict__ h, int64_t hs, float c,
     const uint16_t* __restrict__ w, int64_t n_rows, int hidden, float eps,
     uint16_t* __restrict__ out, int64_t os) {
+  static_assert(NC >= 1 && NC <= LS_NORM_MAX_CHUNKS, "chunks per lane");
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= n_rows) return;
   constexpr bool BF = DT == LS_BF16;
   const int nch = hidden / 8;
   uint16_t* xr = x + row * xs;
-  ls_u32x4 v[LS_NORM_MAX_CHUNKS];
+  ls_u32x4 v[NC], hv[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int ch = min(lane + 64 * i, nch - 1);
+    v[i] = ls_load16(xr + 8 * ch);
+    if constexpr (ADD) hv[i] = ls_load16(h + row * hs + 8 * ch);
+  }
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < LS_NORM_MAX_CHUNKS; ++i) {
-    const int ch = lane + 64 * i;
-    if (ch >= nch) break;
-    v[i] = ls_load16(xr + 8 * ch);
+  for (int i = 0; i < NC; ++i) {
+    if (lane + 64 * i >= nch) break;
     float f[8];
     ls_unpack8(v[i], f, BF);
     if constexpr (ADD) {
       float g[8];
-      ls_unpack8(ls_load16(h + row * hs + 8 * ch), g, BF);
+      ls_unpack8(hv[i], g, BF);
 #pragma unroll
       for (int j = 0; j < 8; ++j) f[j] = ls_round<DT>(__fadd_rn(f[j], ls_round<DT>(__fmul_rn(g[j], c))));
       v[i] = ls_pack8<DT>(f);
-      *reinterpret_cast<ls_u32x4*>(xr + 8 * ch) = v[i];
+      *reinterpret_cast<ls_u32x4*>(xr + 8 * (lane + 64 * i)) = v[i];
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss = __fadd_rn(ss, __fmul_rn(f[j], f[j]));
   }
+  ls_u32x4 wv[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) wv[i] = ls_load16(w + 8 * min(lane + 64 * i, nch - 1));
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
   const float rs = 1.f / sqrtf(__fadd_rn(__fmul_rn(ss, 1.f / (float)hidden), eps));
   uint16_t* orow = out + row * os;
 #pragma unroll
-  for (int i = 0; i < LS_NORM_MAX_CHUNKS; ++i) {
+  for (int i = 0; i < NC; ++i) {
     const int ch = lane + 64 * i;
     if (ch >= nch) break;
     float f[8], wf[8];
     ls_unpack8(v[i], f, BF);
-    ls_unpack8(ls_load16(w + 8 * ch), wf, BF);
+    ls_unpack8(wv[i], wf, BF);
 #pragma unroll
     for (int j = 0; j < 8; ++j) f[j] = __fmul_rn(ls_round<DT>(__fmul_rn(f[j], rs)), wf[j]);
     *reinterpret_cast<ls_u32x4*>(orow + 8 * ch) = ls_pack8<DT>(f);
@@ -295,12 +308,21 @@ int launch_norm(int dtype, uint16_t* x, int64_t xs, const uint16_t* h, int64_t h
                 const uint16_t* w, int64_t n, int hidden, float eps, uint16_t* out, int64_t os,
                 hipStream_t s) {
   const dim3 grid((unsigned)((n + 3) / 4));
-  if (dtype == LS_BF16)
-    hipLaunchKernelGGL((ls_rmsnorm_kernel<LS_BF16, ADD>), grid, dim3(256), 0, s, x, xs, h, hs, c,
-                       w, n, hidden, eps, out, os);
-  else
-    hipLaunchKernelGGL((ls_rmsnorm_kernel<LS_F16, ADD>), grid, dim3(256), 0, s, x, xs, h, hs, c,
-                       w, n, hidden, eps, out, os);
+  const int per_lane = (hidden / 8 + 63) / 64;
+  auto go = [&](auto nc) {
+    constexpr int NC = decltype(nc)::value;
+    if (dtype == LS_BF16)
+      hipLaunchKernelGGL((ls_rmsnorm_kernel<LS_BF16, ADD, NC>), grid, dim3(256), 0, s, x, xs, h,
+                         hs, c, w, n, hidden, eps, out, os);
+    else
+      hipLaunchKernelGGL((ls_rmsnorm_kernel<LS_F16, ADD, NC>), grid, dim3(256), 0, s, x, xs, h,
+                         hs, c, w, n, hidden, eps, out, os);
+  };
+  if (per_lane <= 1) go(std::integral_constant<int, 1>());
+  else if (per_lane <= 2) go(std::integral_constant<int, 2>());
+  else if (per_lane <= 4) go(std::integral_constant<int, 4>());
+  else if (per_lane <= 8) go(std::integral_constant<int, 8>());
+  else go(std::integral_constant<int, LS_NORM_MAX_CHUNKS>());
   return ls_check_launch("ls_rmsnorm_kernel");
 }
 
