@@ -102,7 +102,12 @@ __global__ void ls_attn_plan_kernel(const int32_t* __restrict__ cu_q,
 #define LS_ATT_KBYTES (64 * 256)             // K page: 64 rows x 256 B
 #define LS_ATT_STAGE_BYTES (2 * LS_ATT_KBYTES)  // + V^T page: 128 rows x 128 B
 #define LS_ATT_WORDS (LS_ATTN_MAX_PAGES / 32)
+#ifndef LS_ATT_XCD_CHUNK
 #define LS_ATT_XCD_CHUNK 32                  // consecutive tiles per XCD run
+#endif
+#ifndef LS_ATT_SPIN_SLEEP
+#define LS_ATT_SPIN_SLEEP 1                  // s_sleep units between a waiting wave's polls
+#endif
 #define LS_ATT_MAX_UNION (LS_ATT_TILE * LS_ATTN_MAX_TAKE)
 
 typedef _Float16 ls_half2 __attribute__((ext_vector_type(2)));
@@ -615,7 +620,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       // in the status word and goes on; the host turns that into an error.
       bool landed = false;
       for (int spin = 0; spin < spin_limit; ++spin) {
-        if (!try_claim(ui)) __builtin_amdgcn_s_sleep(1);
+        if (!try_claim(ui)) __builtin_amdgcn_s_sleep(LS_ATT_SPIN_SLEEP);
         sw = stage_word(ui);
         if (is_ready(ui, sw)) {
           landed = true;
