@@ -197,7 +197,10 @@ typedef __attribute__((address_space(3))) void ls_lds_void;
 // drain the whole prefetch queue); callers order the copies themselves with
 // vmcnt waits and barriers or ready tokens.  An SALU write of M0 followed by a
 // global load with LDS destination needs one wait state, which the compiler
-// cannot insert inside the asm block.
+// cannot insert inside the asm block.  M0 is listed as clobbered, which the
+// compiler notes it may not honour for a reserved register: every copy sets
+// M0 itself, and no code of these kernels keeps a value in M0 across one (no
+// indexed register moves, GWS, append/consume or messages).
 __device__ __forceinline__ void ls_dma16(const void* sbase, uint32_t voff, uint32_t lds_off) {
   const uint64_t a = (uint64_t)(uintptr_t)sbase;
   // (readfirstlane returns int: widen each half as unsigned, or the low half
