@@ -15,7 +15,10 @@
 // scores (infllmv2_attn_stage1, third_party/infllmv2/paper1.patch:1103-1302,
 // 2340-2362), and infllmv2_attn_with_kvcache with topk_idx
 // (paper1.patch:2511-2615).
+#include <type_traits>
+
 #include "ls_common.h"
+#include "ls_topk_row.h"
 
 #define LS_TID ((int)__builtin_amdgcn_workitem_id_x())
 #define LS_BID_X ((int)__builtin_amdgcn_workgroup_id_x())
@@ -401,6 +404,30 @@ __global__ __launch_bounds__(256) void ls_decode_topk_kernel(
   }
   for (int i = kept + tid; i < take; i += 256) orow[i] = -1;
 }
+// The same selection for rows of at most 64 * KPL pages, one wave per (row,
+// group): the prefill path's wave-level top-k (the lanes' two largest keys
+// bound the take-th key from below, the keys above the bound are gathered
+// with their pages and bisected) over the whole pooled row, written in page
+// order with the ids above q_idx as -1 (the ascending list's tail).
+template <int KPL>
+__global__ __launch_bounds__(256) void ls_decode_topk_wave_kernel(
+    const uint16_t* __restrict__ pooled, const int32_t* __restrict__ cu_q, int batch,
+    int64_t total_q, int G, const int32_t* __restrict__ cache_seqlens, int out_len,
+    int block_size, int take, int32_t* __restrict__ ids) {
+  __shared__ uint32_t s_scr[4][320];  // per-wave gather space
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + wv;  // g * total_q + t
+  if (row >= (int64_t)G * total_q) return;
+  const int g = (int)(row / total_q);
+  const int64_t t = row - (int64_t)g * total_q;
+  const int b = ls_find_segment(cu_q, batch, t);
+  const int64_t q_idx =
+      ((int64_t)cache_seqlens[b] - (cu_q[b + 1] - cu_q[b]) + (t - cu_q[b])) / block_size;
+  ls_topk_select16<KPL>(pooled, row * out_len, out_len, take, 0, lane, ids + row * take,
+                        s_scr[wv], (int)min(q_idx, (int64_t)INT32_MAX));
+}
+
 // ---------------------------------------------------------------------------
 // Split-K attention over the cache.  Workgroup (split s, row t, group g) has
 // four waves; wave w runs the pages of plan slots
@@ -813,6 +840,22 @@ extern "C" int ls_decode_select(const void* q, int64_t q_row_stride, const int32
                        local_blocks, pooled);
   rc = ls_check_launch("ls_stage1_pool_kernel");
   if (rc) return rc;
+  // Rows of up to 8192 pages: one wave per row; longer rows: one workgroup
+  // per row with the keys in LDS.
+  if (out_len <= 8192) {
+    const dim3 gw((unsigned)(((int64_t)num_kv_heads * total_q + 3) / 4));
+    auto go = [&](auto kpl) {
+      hipLaunchKernelGGL((ls_decode_topk_wave_kernel<decltype(kpl)::value>), gw, dim3(256), 0, s,
+                         pooled, cu_seqlens_q, batch, total_q, num_kv_heads, cache_seqlens,
+                         (int)out_len, block_size, take, topk_idx);
+    };
+    if (out_len <= 256) go(std::integral_constant<int, 4>());
+    else if (out_len <= 1024) go(std::integral_constant<int, 16>());
+    else if (out_len <= 2048) go(std::integral_constant<int, 32>());
+    else if (out_len <= 4096) go(std::integral_constant<int, 64>());
+    else go(std::integral_constant<int, 128>());
+    return ls_check_launch("ls_decode_topk_wave_kernel");
+  }
   const size_t key_bytes = ((size_t)out_len * 2 + 3) & ~(size_t)3;
   hipLaunchKernelGGL(ls_decode_topk_kernel, dim3((unsigned)total_q, num_kv_heads), dim3(256),
                      key_bytes, s, pooled, cu_seqlens_q, batch, total_q, cache_seqlens,

@@ -12,6 +12,7 @@
 // scores (rounding is monotone, so the max is rounded once).
 #include "ls_common.h"
 #include "ls_nosa_internal.h"
+#include "ls_topk_row.h"
 
 // ---------------------------------------------------------------------------
 // Fused weights
@@ -810,201 +811,6 @@ __global__ __launch_bounds__(256) void ls_score_f32_kernel(
 }
 
 
-// ---------------------------------------------------------------------------
-// Top-k page selection.  One wave per (group, token) row.  The k'-th largest
-// order-preserving key T is found by bisection over the key bits, counting
-// with ballots over keys held in registers; pages above T and the first
-// (lowest-index) pages equal to T are emitted in ascending order between the
-// sink pages and the local pages.
-// ---------------------------------------------------------------------------
-// Top-kk of one row's cn candidate scores (columns base .. base + cn - 1 of
-// P), held as order-preserving keys in NS register slots of 64 lanes.  Loads
-// are issued together (addresses clamped into the row), then converted; keys
-// of lanes past cn are 0, which no threshold candidate (>= 1) counts.  The
-// kk-th largest key T is found by bisection over the key bits with ballot
-// counts; the winners (key > T, then the first kk - #{key > T} keys equal to
-// T in page order) are written in page order after the lo_end sink pages.
-template <int NS, bool KEY32>
-__device__ __forceinline__ void ls_topk_row(const void* __restrict__ P, int64_t base, int cn,
-                                            int kk, int lo_end, int lane,
-                                            int32_t* __restrict__ orow,
-                                            uint32_t* __restrict__ scr) {
-  uint32_t key[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const int c = min(s * 64 + lane, cn - 1);
-    if constexpr (KEY32) key[s] = ((const uint32_t*)P)[base + c];
-    else key[s] = ((const uint16_t*)P)[base + c];
-  }
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    uint32_t k;
-    if constexpr (KEY32) k = ls_order_key32(key[s]);
-    else k = ls_order_key16((uint16_t)key[s]);
-    key[s] = s * 64 + lane < cn ? k : 0u;
-  }
-  const uint32_t T = ls_kth_key_row<NS, KEY32 ? 32 : 16>(key, kk, scr, lane);
-  int gt = 0;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) gt += __popcll(__ballot(key[s] > T));
-  const int m = kk - gt;
-
-  int out_pos = lo_end, eq_before = 0;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const int c = s * 64 + lane;
-    const bool valid = c < cn;
-    const bool eq = valid && key[s] == T;
-    const uint64_t eq_mask = __ballot(eq);
-    const int eq_rank = eq_before + ls_lanes_below(eq_mask);
-    const bool sel = valid && (key[s] > T || (eq && eq_rank < m));
-    const uint64_t sel_mask = __ballot(sel);
-    const int pos = out_pos + ls_lanes_below(sel_mask);
-    if (sel && pos < lo_end + kk) orow[pos] = lo_end + c;  // exactly kk by construction
-    out_pos += __popcll(sel_mask);
-    eq_before += __popcll(eq_mask);
-  }
-}
-
-// The end of ls_topk_row16 for n gathered candidates (key << 16 | column,
-// in column order) held in NP slots of the wave's scratch: the kk-th key T
-// bisected from the common bit prefix of lo and the row maximum m1 (per-lane
-// maxima, reduced here), then the chosen columns written in column order.
-template <int NP>
-__device__ __forceinline__ void ls_topk_emit_packed(const uint32_t* __restrict__ scr, int n,
-                                                    uint32_t lo, uint32_t m1, int kk, int lo_end,
-                                                    int lane, int32_t* __restrict__ orow) {
-  uint32_t pk[NP];
-#pragma unroll
-  for (int i = 0; i < NP; ++i) pk[i] = i * 64 + lane < n ? scr[i * 64 + lane] : 0u;
-  uint32_t hi = m1;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, LS_WAVE));
-  hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)hi);
-  // T: the largest 16-bit key with #{key >= T} >= kk, sharing lo's and hi's
-  // common bit prefix.
-  uint32_t T = lo;
-  const uint32_t d = lo ^ hi;
-  if (d != 0u) {
-    const int tb = 31 - __builtin_clz(d);
-    T = lo & ~((2u << tb) - 1u);
-#pragma unroll 1
-    for (int bit = tb; bit >= 0; --bit) {
-      const uint32_t cand = (T | (1u << bit)) << 16;
-      int cnt = 0;
-#pragma unroll
-      for (int i = 0; i < NP; ++i) cnt += __popcll(__ballot(pk[i] >= cand));
-      if (cnt >= kk) T |= 1u << bit;
-    }
-  }
-  const uint32_t above = (T << 16) | 0xffffu;  // packed keys above T
-  int gt = 0;
-#pragma unroll
-  for (int i = 0; i < NP; ++i) gt += __popcll(__ballot(pk[i] > above));
-  const int m = kk - gt;
-  int out_pos = lo_end, eq_before = 0;
-#pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const bool valid = i * 64 + lane < n;
-    const bool eq = valid && (pk[i] >> 16) == T;
-    const uint64_t eq_mask = __ballot(eq);
-    const int eq_rank = eq_before + ls_lanes_below(eq_mask);
-    const bool sel = valid && (pk[i] > above || (eq && eq_rank < m));
-    const uint64_t sel_mask = __ballot(sel);
-    const int pos = out_pos + ls_lanes_below(sel_mask);
-    if (sel && pos < lo_end + kk) orow[pos] = lo_end + (int)(pk[i] & 0xffffu);
-    out_pos += __popcll(sel_mask);
-    eq_before += __popcll(eq_mask);
-  }
-}
-
-// The same for 16-bit scores of rows of more than four slots, emitting from
-// the gathered candidates: the keys >= lo (lo = the kk-th largest of the
-// lanes' two largest keys, a lower bound of the kk-th key) are packed as
-// key << 16 | column into at most four slots in column order, the kk-th key T
-// is bisected on them from the common bit prefix of lo and the row maximum,
-// and the chosen columns (keys > T, then the lowest-column ties) are written
-// from those four slots instead of from all NS.  When more than 256 keys pass
-// (or no bound exists) the row is searched and emitted over all NS slots.
-template <int NS>
-__device__ __forceinline__ void ls_topk_row16(const void* __restrict__ P, int64_t base, int cn,
-                                              int kk, int lo_end, int lane,
-                                              int32_t* __restrict__ orow,
-                                              uint32_t* __restrict__ scr) {
-  if (NS <= 4 || kk < 1 || kk > 128)
-    return ls_topk_row<NS, false>(P, base, cn, kk, lo_end, lane, orow, scr);
-  // Keys are held shifted up by 16 (order key << 16), so a gathered entry is
-  // key | column; 0 marks a column past the row.  Only the slots that reach
-  // the row's end (a uniform test) pay for the per-lane column check.
-  cn = __builtin_amdgcn_readfirstlane(cn);
-  uint32_t key[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) key[s] = ((const uint16_t*)P)[base + min(s * 64 + lane, cn - 1)];
-  const int n_full = cn >> 6;  // slots lying wholly inside the row (uniform)
-  uint32_t m1 = 0u, m2 = 0u;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const uint32_t b = key[s];
-    uint32_t k = (b ^ ((b >> 15) * 0x7fffu) ^ 0x8000u) << 16;  // ls_order_key16(b) << 16
-    if (s >= n_full) k = s * 64 + lane < cn ? k : 0u;
-    key[s] = k;
-    m2 = max(m2, min(m1, k));
-    m1 = max(m1, k);
-  }
-  m1 >>= 16;
-  m2 >>= 16;
-  const uint32_t mm[2] = {m1, m2};
-  const uint32_t lo = ls_kth_bisect<2>(mm, kk, 0u, 15);
-  // Gather the keys >= lo with their columns, in column order; stop once more
-  // than 256 have been found (the scratch holds 256 + 63).
-  int n = 0;
-  if (lo != 0u) {
-    const uint32_t lo_sh = lo << 16;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      if (n <= 256) {
-        const bool sv = key[s] >= lo_sh;
-        const uint64_t mk = __ballot(sv);
-        const int pos = (int)__builtin_amdgcn_mbcnt_hi(
-            (uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, (uint32_t)n));
-        if (sv) scr[pos] = key[s] | (uint32_t)(s * 64 + lane);
-        n += __popcll(mk);
-      }
-    }
-  }
-  if (lo == 0u || n > 256) {  // no usable bound: every slot is searched and emitted
-#pragma unroll
-    for (int s = 0; s < NS; ++s) key[s] >>= 16;
-    // (The row length is re-read through an empty asm so that the column
-    // checks below are formed here, not kept alive from the loop above.)
-    asm volatile("" : "+s"(cn));
-    const uint32_t T = ls_kth_bisect<NS>(key, kk, 0u, 15);
-    int gt = 0;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) gt += __popcll(__ballot(key[s] > T));
-    const int m = kk - gt;
-    int out_pos = lo_end, eq_before = 0;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const int c = s * 64 + lane;
-      const bool valid = c < cn;
-      const bool eq = valid && key[s] == T;
-      const uint64_t eq_mask = __ballot(eq);
-      const int eq_rank = eq_before + ls_lanes_below(eq_mask);
-      const bool sel = valid && (key[s] > T || (eq && eq_rank < m));
-      const uint64_t sel_mask = __ballot(sel);
-      const int pos = out_pos + ls_lanes_below(sel_mask);
-      if (sel && pos < lo_end + kk) orow[pos] = lo_end + c;
-      out_pos += __popcll(sel_mask);
-      eq_before += __popcll(eq_mask);
-    }
-    return;
-  }
-  if (n <= 64) return ls_topk_emit_packed<1>(scr, n, lo, m1, kk, lo_end, lane, orow);
-  if (n <= 128) return ls_topk_emit_packed<2>(scr, n, lo, m1, kk, lo_end, lane, orow);
-  return ls_topk_emit_packed<4>(scr, n, lo, m1, kk, lo_end, lane, orow);
-}
-
 template <int KPL, bool KEY32>
 __global__ __launch_bounds__(256) void ls_topk_kernel(
     const void* __restrict__ P, int64_t p_stride, const int32_t* __restrict__ cu_q,
@@ -1050,38 +856,18 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
   // Candidates in registers, NS slots of 64; the row's slot count is uniform,
   // so the branch picks one straight-line body per wave.
   const int64_t base = row * p_stride + lo_end;
-  const int n_slots = (cn + 63) >> 6;
-  if (n_slots <= 1) return ls_topk_row<1, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
-  if (n_slots <= 2) return ls_topk_row<2, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
-  if (n_slots <= 4 || KPL <= 4) return ls_topk_row<(KPL < 4 ? KPL : 4), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
   if constexpr (!KEY32) {
-    // Slot counts in steps of about an eighth, so a row runs few empty slots.
-#define LS_TOPK16_CASE(N)                                                                  \
-  if (n_slots <= (N) || KPL <= (N))                                                        \
-    return ls_topk_row16<(KPL < (N) ? KPL : (N))>(P, base, cn, kk, lo_end, lane, orow, scr);
-    LS_TOPK16_CASE(6)
-    LS_TOPK16_CASE(8)
-    LS_TOPK16_CASE(10)
-    LS_TOPK16_CASE(12)
-    LS_TOPK16_CASE(14)
-    LS_TOPK16_CASE(16)
-    LS_TOPK16_CASE(20)
-    LS_TOPK16_CASE(24)
-    LS_TOPK16_CASE(28)
-    LS_TOPK16_CASE(32)
-    LS_TOPK16_CASE(40)
-    LS_TOPK16_CASE(48)
-    LS_TOPK16_CASE(56)
-    LS_TOPK16_CASE(64)
-    LS_TOPK16_CASE(96)
-#undef LS_TOPK16_CASE
-    return ls_topk_row16<KPL>(P, base, cn, kk, lo_end, lane, orow, scr);
+    return ls_topk_select16<KPL>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
   } else {
-    if (n_slots <= 8 || KPL <= 8) return ls_topk_row<(KPL < 8 ? KPL : 8), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
-    if (n_slots <= 16 || KPL <= 16) return ls_topk_row<(KPL < 16 ? KPL : 16), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
-    if (n_slots <= 32 || KPL <= 32) return ls_topk_row<(KPL < 32 ? KPL : 32), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
-    if (n_slots <= 64 || KPL <= 64) return ls_topk_row<(KPL < 64 ? KPL : 64), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
-    return ls_topk_row<KPL, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr);
+    const int n_slots = (cn + 63) >> 6;
+    if (n_slots <= 1) return ls_topk_row<1, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
+    if (n_slots <= 2) return ls_topk_row<2, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
+    if (n_slots <= 4 || KPL <= 4) return ls_topk_row<(KPL < 4 ? KPL : 4), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
+    if (n_slots <= 8 || KPL <= 8) return ls_topk_row<(KPL < 8 ? KPL : 8), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
+    if (n_slots <= 16 || KPL <= 16) return ls_topk_row<(KPL < 16 ? KPL : 16), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
+    if (n_slots <= 32 || KPL <= 32) return ls_topk_row<(KPL < 32 ? KPL : 32), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
+    if (n_slots <= 64 || KPL <= 64) return ls_topk_row<(KPL < 64 ? KPL : 64), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
+    return ls_topk_row<KPL, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
   }
 }
 

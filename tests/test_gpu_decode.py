@@ -115,6 +115,39 @@ def test_decode_select_matches_oracle(dtype, len_q):
                 assert kept == sorted(set(kept)) and row == kept + [-1] * (len(row) - len(kept))
 
 
+@pytest.mark.parametrize("lens,len_q", [
+    ([131072, 50000, 7000, 300], 1),    # 2048 pages: one wave per row, gathered candidates
+    ([70000, 20000], 3),                # 1141 pages, several rows per sequence
+    ([600000, 20000], 1),               # 9375 pages: one workgroup per row, keys in LDS
+])
+def test_decode_select_long_rows_match_oracle(lens, len_q):
+    cap = max(lens)
+    k, v, kc, kp, vp = _filled_cache(lens, cap, seed=5)
+    del k, v, kp, vp
+    B, H = len(lens), 32
+    g = torch.Generator().manual_seed(6)
+    cu_q = _cu([len_q] * B)
+    q = torch.randn(cu_q[-1], H, D, generator=g).to(torch.bfloat16)
+    for topk, local in [(64, 4), (128, 1)]:
+        ids = decode_topk_idx(q.to(DEV), kc, _i32(lens), _i32(cu_q), topk=topk,
+                              local_blocks=local, init_blocks=1).cpu()
+        kc_packed = torch.cat([kc[b, :n_windows(L)].cpu() for b, L in enumerate(lens)])
+        cu_kc = _cu([n_windows(L) for L in lens])
+        want, pooled = oracle.decode_select(q, kc_packed, cu_q, cu_kc, lens,
+                                            topk=topk, local_blocks=local, init_blocks=1,
+                                            return_scores=True)
+        assert ids.shape == want.shape
+        rep = oracle.check_topk(ids, want, pooled, torch.bfloat16, ulp_band=1.0)
+        print(f"decode select lens={lens} len_q={len_q} topk={topk}: {rep}")
+        assert rep.ok, str(rep)
+        assert rep.exact_rows == rep.rows, str(rep)
+        for gg in range(G):
+            for r in range(cu_q[-1]):
+                row = ids[gg, r].tolist()
+                kept = [x for x in row if x >= 0]
+                assert kept == sorted(set(kept)) and row == kept + [-1] * (len(row) - len(kept))
+
+
 def _packed(k, v, lens):
     return (torch.cat([k[b, :L].cpu() for b, L in enumerate(lens)]),
             torch.cat([v[b, :L].cpu() for b, L in enumerate(lens)]))
