@@ -612,12 +612,15 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   // The next page's union entry is read before the current page is computed.
   int ui = next_page(-1);
   uint32_t meta = ui < n_union ? s_umeta[ui] : 0u;
+  bool expired = false;  // a wait of this wave ran out (uniform)
   while (ui < n_union) {
     uint64_t sw = stage_word(ui);
     if (!is_ready(ui, sw)) {
       // Bounded wait (the protocol cannot deadlock; the bound only guarantees
       // that a wave always finishes).  A wave whose wait expires reports it
-      // in the status word and goes on; the host turns that into an error.
+      // in the status word, goes on, and writes NaN for its rows, so the
+      // failure also shows where the host cannot read the status (a replayed
+      // graph); the host turns the status into an error.
       bool landed = false;
       for (int spin = 0; spin < spin_limit; ++spin) {
         if (!try_claim(ui)) __builtin_amdgcn_s_sleep(LS_ATT_SPIN_SLEEP);
@@ -627,9 +630,12 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
           break;
         }
       }
-      if (!landed && lane == 0)
-        __hip_atomic_fetch_or(status, LS_ATTN_RING_TIMEOUT, __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
+      if (!landed) {
+        expired = true;
+        if (lane == 0)
+          __hip_atomic_fetch_or(status, LS_ATTN_RING_TIMEOUT, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
 
     const int nxt = next_page(ui);
@@ -656,6 +662,13 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     const int64_t t = t0 + row;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     uint16_t* orow = out + (t * G * gs + (int64_t)g * gs + head) * D + 4 * q;
+    if (expired) {  // quiet-NaN bit patterns (this file assumes no NaN arithmetic)
+      const uint32_t nan2 = DT == LS_BF16 ? 0x7fc07fc0u : 0x7e007e00u;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) *reinterpret_cast<uint2*>(orow + 16 * db) = make_uint2(nan2, nan2);
+      if (lse && q == 0) lse[((int64_t)g * gs + head) * total_q + t] = __uint_as_float(0x7fc00000u);
+      continue;
+    }
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
       const uint32_t lo = ls_pack2(LsElem<DT>::from_f(o[j][db][0] * inv), LsElem<DT>::from_f(o[j][db][1] * inv));

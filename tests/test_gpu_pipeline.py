@@ -238,16 +238,50 @@ def test_end_to_end_prefill_32k_sampled():
 
 def test_ring_wait_expiry_is_reported():
     """With the wait bound forced to zero from the host every ring wait expires at
-    once: the kernel still finishes, the status word is set and the wrapper raises.
-    The next call with the default bound is clean and correct."""
+    once: the kernel still finishes, the status word is set and the wrapper raises,
+    and the rows of the waves whose wait expired are NaN.  The next call with the
+    default bound is clean and correct."""
     case, ids = _attention_case(lens=(3000,), seed=4)
     L = _hip.lib()
+    out = torch.zeros_like(case.q)
     L.ls_attn_set_spin_limit(0)
     try:
         with pytest.raises(RuntimeError, match="expired"):
             sparse_attention(case.q, case.k, case.v, case.cu_seqlens, case.cu_seqlens,
-                             3000, 3000, ids)
+                             3000, 3000, ids, out=out)
     finally:
         L.ls_attn_set_spin_limit(-1)
+    nan_rows = torch.isnan(out.float()).any(dim=2).any(dim=1)
+    assert bool(nan_rows.any())
+    # a row is either NaN in every head of a group or has finite values there
+    per_group = torch.isnan(out.float()).any(dim=2).view(out.shape[0], 2, -1)
+    assert bool((per_group.all(dim=2) == per_group.any(dim=2)).all())
     rows = spread_rows(case.cu_host, per_seq=32)
     _check_attention(case, ids, rows)
+
+
+def test_sparse_attention_graph_replays_match_eager():
+    """The attention call captured in a HIP graph (workspace and plans formed by
+    kernels, no memset nodes, no host read under capture): three replays, with
+    eager calls and a clear of the output between them, each equal to the eager
+    result bit for bit."""
+    case, ids = _attention_case(lens=(3000, 1300), seed=6)
+    args = (case.q, case.k, case.v, case.cu_seqlens, case.cu_seqlens, 3000, 3000, ids)
+    want = sparse_attention(*args)
+    out = torch.empty_like(want)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        sparse_attention(*args, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        sparse_attention(*args, out=out)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        assert torch.equal(sparse_attention(*args), want)
