@@ -260,6 +260,40 @@ def test_ring_wait_expiry_is_reported():
     _check_attention(case, ids, rows)
 
 
+def test_prefill_step_graph_replays_match_eager():
+    """The whole step (compressed keys, selection, attention), with the host
+    offsets given, captured in one HIP graph: three replays, with an eager step
+    between them, each giving the eager step's plans and output bit for bit."""
+    case = workloads.hidden_space_layer((2500, 1100), device=DEV, seed=12)
+
+    def step():
+        return leanselect_sparse_prefill(
+            case.q, case.k, case.v, case.cu_seqlens, case.selector, topk=case.topk,
+            local_blocks=case.local_blocks, init_blocks=case.init_blocks,
+            cu_seqlens_host=case.cu_host, return_topk_idx=True)
+
+    want_out, want_ids = step()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g, ids_g = step()
+    for _ in range(3):
+        out_g.zero_()
+        ids_g.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ids_g, want_ids)
+        assert torch.equal(out_g, want_out)
+        out_e, ids_e = step()
+        assert torch.equal(ids_e, want_ids) and torch.equal(out_e, want_out)
+
+
 def test_sparse_attention_graph_replays_match_eager():
     """The attention call captured in a HIP graph (workspace and plans formed by
     kernels, no memset nodes, no host read under capture): three replays, with
