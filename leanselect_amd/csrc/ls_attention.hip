@@ -612,15 +612,13 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   // The next page's union entry is read before the current page is computed.
   int ui = next_page(-1);
   uint32_t meta = ui < n_union ? s_umeta[ui] : 0u;
-  bool expired = false;  // a wait of this wave ran out (uniform)
   while (ui < n_union) {
     uint64_t sw = stage_word(ui);
     if (!is_ready(ui, sw)) {
       // Bounded wait (the protocol cannot deadlock; the bound only guarantees
       // that a wave always finishes).  A wave whose wait expires reports it
-      // in the status word, goes on, and writes NaN for its rows, so the
-      // failure also shows where the host cannot read the status (a replayed
-      // graph); the host turns the status into an error.
+      // in the status word and goes on; the host turns the status into an
+      // error, and the epilogue below writes NaN rows once it is set.
       bool landed = false;
       for (int spin = 0; spin < spin_limit; ++spin) {
         if (!try_claim(ui)) __builtin_amdgcn_s_sleep(LS_ATT_SPIN_SLEEP);
@@ -630,12 +628,9 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
           break;
         }
       }
-      if (!landed) {
-        expired = true;
-        if (lane == 0)
-          __hip_atomic_fetch_or(status, LS_ATTN_RING_TIMEOUT, __ATOMIC_RELAXED,
-                                __HIP_MEMORY_SCOPE_AGENT);
-      }
+      if (!landed && lane == 0)
+        __hip_atomic_fetch_or(status, LS_ATTN_RING_TIMEOUT, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
     }
 
     const int nxt = next_page(ui);
@@ -653,6 +648,12 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   LS_WAIT_VMCNT(0);  // no copy of this wave may land after the workgroup ends
 
   // ---- epilogue ----
+  // A wait that expired (this wave's, or any earlier one seen here) makes the
+  // rows NaN, so the failure also shows where the host cannot read the status
+  // word (a replayed graph).  Read once per wave, after the loop.
+  const bool expired = (__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
+                            status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) &
+                        LS_ATTN_RING_TIMEOUT) != 0;
 #pragma unroll
   for (int j = 0; j < LS_ATT_TPW; ++j) {
     const int row = w * LS_ATT_TPW + j;
