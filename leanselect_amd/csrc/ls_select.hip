@@ -439,7 +439,9 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_mfma_kernel(
     n_atoms = (int64_t)cu_a[b + 1] - a0;
     if constexpr (MODE == LS_SCORE_SELECT) {
       p_lo = init_blocks;
-      p_hi = qb - local_blocks - 1;
+      // (Clamped to the row's columns: a max_seqlen_q below a sequence's
+      // length then gives wrong pages, never a write outside the row.)
+      p_hi = (int)min((int64_t)(qb - local_blocks - 1), out_stride - 1);
     } else {  // full_seq_len carries the page-column count in this mode
       p_lo = 0;
       p_hi = (int)min(n_atoms / 4, full_seq_len - 1);
@@ -618,7 +620,9 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_panel_kernel(
     n_atoms = (int64_t)cu_a[b + 1] - a0;
     if constexpr (MODE == LS_SCORE_SELECT) {
       p_lo = init_blocks;
-      p_hi = qb - local_blocks - 1;
+      // (Clamped to the row's columns: a max_seqlen_q below a sequence's
+      // length then gives wrong pages, never a write outside the row.)
+      p_hi = (int)min((int64_t)(qb - local_blocks - 1), out_stride - 1);
     } else {  // full_seq_len carries the page-column count in this mode
       p_lo = 0;
       p_hi = (int)min(n_atoms / 4, full_seq_len - 1);
@@ -847,7 +851,8 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
     return;
   }
   const int kk = n_valid - n_forced;
-  const int cn = hi_start - lo_end;
+  // (Clamped to the row's columns, as the scoring is.)
+  const int cn = (int)min((int64_t)(hi_start - lo_end), p_stride - lo_end);
 
   for (int i = lane; i < lo_end; i += 64) orow[i] = i;
   const int hi_pos = lo_end + kk;
