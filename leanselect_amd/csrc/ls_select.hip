@@ -117,14 +117,16 @@ __global__ __launch_bounds__(256) void ls_proj_mfma_kernel(
 template <int DT, int FB>
 __global__ __launch_bounds__(256, 2) void ls_proj_tile_kernel(
     const uint16_t* __restrict__ A, int64_t lda, int64_t gk, int64_t M, int K,
-    const uint16_t* __restrict__ wt, uint16_t* __restrict__ out) {
+    const uint16_t* __restrict__ wt, uint16_t* __restrict__ out, int G) {
   constexpr int F = FB * 16;
   constexpr int NB = F * 16 / 256;  // 16-byte weight chunks per thread per K step
   __shared__ ls_u32x4 sB[2][F * 16];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int r = lane & 15, q = lane >> 4;
-  const int g = blockIdx.y;
-  const int64_t m0 = (int64_t)blockIdx.x * 128 + w * 32;
+  // The groups of one 128-row tile are neighbouring workgroups, so the halves
+  // of each row are read close together in time.
+  const int g = (int)(blockIdx.x % (unsigned)G);
+  const int64_t m0 = (int64_t)(blockIdx.x / (unsigned)G) * 128 + w * 32;
   const uint16_t* Ag = A + g * gk;
   const uint16_t* Wg = wt + (int64_t)g * F * K;
   const uint16_t* a0p = Ag + min(m0 + r, M - 1) * lda + 8 * q;
@@ -965,10 +967,11 @@ int launch_proj16(const void* A, int64_t lda, int64_t gk, int64_t M, int K, int 
   const uint16_t* w = (const uint16_t*)wt;
   uint16_t* o = (uint16_t*)out;
   if (K % 128 == 0 && F % 64 == 0 && F <= 128) {  // LDS-staged weight tiles
+    const dim3 tgrid((unsigned)((M + 127) / 128 * G));
     if (F == 64)
-      hipLaunchKernelGGL((ls_proj_tile_kernel<DT, 4>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o);
+      hipLaunchKernelGGL((ls_proj_tile_kernel<DT, 4>), tgrid, dim3(256), 0, s, a, lda, gk, M, K, w, o, G);
     else
-      hipLaunchKernelGGL((ls_proj_tile_kernel<DT, 8>), grid, dim3(256), 0, s, a, lda, gk, M, K, w, o);
+      hipLaunchKernelGGL((ls_proj_tile_kernel<DT, 8>), tgrid, dim3(256), 0, s, a, lda, gk, M, K, w, o, G);
     return ls_check_launch("ls_proj_tile_kernel");
   }
   switch (F / 16) {
