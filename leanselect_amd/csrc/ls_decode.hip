@@ -241,20 +241,37 @@ __global__ __launch_bounds__(256) void ls_stage1_pool_kernel(
     const float* prow = part + ((int64_t)g * total_q + t) * n_chunks * 32;
     const int nch = (nc + 63) / 64;
     const int h = tid >> 4, share = tid & 15;
-    // (Unrolled so that each thread's partial loads are in flight together.)
+    // A thread's first eight (max, sum) pairs (chunks share + 16 i: all of
+    // them up to 128 chunks) are loaded once, together, and kept for the sum;
+    // chunks beyond are read in the loops.
+    constexpr int NP = 8;
+    float pm[NP], pl[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int c = share + 16 * i;
+      const bool ok = h < gs && c < nch;
+      const float2 v = ok ? *reinterpret_cast<const float2*>(prow + c * 32 + 2 * h)
+                          : make_float2(-INFINITY, 0.f);
+      pm[i] = v.x;
+      pl[i] = v.y;
+    }
     float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) M = fmaxf(M, pm[i]);
     if (h < gs)
-#pragma unroll 8
-      for (int c = share; c < nch; c += 16) M = fmaxf(M, prow[c * 32 + 2 * h]);
+      for (int c = share + 16 * NP; c < nch; c += 16) M = fmaxf(M, prow[c * 32 + 2 * h]);
 #pragma unroll
     for (int o = 8; o >= 1; o >>= 1) M = fmaxf(M, ls_shfl_xor(M, o));
     float L = 0.f;
-    if (h < gs && M != -INFINITY)
-#pragma unroll 8
-      for (int c = share; c < nch; c += 16) {
+    if (h < gs && M != -INFINITY) {
+#pragma unroll
+      for (int i = 0; i < NP; ++i)
+        if (pm[i] != -INFINITY) L += pl[i] * __builtin_amdgcn_exp2f(pm[i] - M);
+      for (int c = share + 16 * NP; c < nch; c += 16) {
         const float mc = prow[c * 32 + 2 * h];
         if (mc != -INFINITY) L += prow[c * 32 + 2 * h + 1] * __builtin_amdgcn_exp2f(mc - M);
       }
+    }
 #pragma unroll
     for (int o = 8; o >= 1; o >>= 1) L += ls_shfl_xor(L, o);
     if (h < gs && share == 0) s_lse[h] = M + __log2f(L);
