@@ -445,6 +445,102 @@ __global__ __launch_bounds__(256) void ls_decode_topk_wave_kernel(
                         s_scr[wv], (int)min(q_idx, (int64_t)INT32_MAX));
 }
 
+// The same selection with the four waves of a workgroup sharing one (row,
+// group), for rows of 5 to 4 * 64 * NSW pages and take <= 128: wave w holds
+// slots [w NSW, (w + 1) NSW) of the row (16-bit order keys << 16), the lanes'
+// two largest keys of all four waves bound the take-th key from below (lo),
+// each wave gathers its keys >= lo packed with their page, in page order after
+// the waves before it, and wave 0 bisects and emits from the gathered keys.
+// More than 256 keys above the bound (or none) hands the row to the one-wave
+// selection.
+template <int NSW>
+__global__ __launch_bounds__(256) void ls_decode_topk_wg_kernel(
+    const uint16_t* __restrict__ pooled, const int32_t* __restrict__ cu_q, int batch,
+    int64_t total_q, int G, const int32_t* __restrict__ cache_seqlens, int out_len,
+    int block_size, int take, int32_t* __restrict__ ids) {
+  __shared__ uint32_t s_m[2][256];   // each lane's two largest keys (<< 16)
+  __shared__ uint32_t s_scr[320];    // gathered key | page, page order
+  __shared__ int s_cnt[4];
+  __shared__ uint32_t s_lo;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t row = blockIdx.x;  // g * total_q + t
+  const int g = (int)(row / total_q);
+  const int64_t t = row - (int64_t)g * total_q;
+  const int cn = out_len;
+  const uint16_t* rowp = pooled + row * out_len;
+  int32_t* orow = ids + row * take;
+  const int b = ls_find_segment(cu_q, batch, t);
+  const int64_t q_idx =
+      ((int64_t)cache_seqlens[b] - (cu_q[b + 1] - cu_q[b]) + (t - cu_q[b])) / block_size;
+  const int id_max = (int)min(q_idx, (int64_t)INT32_MAX);
+  uint32_t key[NSW];
+#pragma unroll
+  for (int s = 0; s < NSW; ++s) key[s] = rowp[min((w * NSW + s) * 64 + lane, cn - 1)];
+  uint32_t m1 = 0u, m2 = 0u;
+#pragma unroll
+  for (int s = 0; s < NSW; ++s) {
+    const uint32_t b16 = key[s];
+    uint32_t k = (b16 ^ ((b16 >> 15) * 0x7fffu) ^ 0x8000u) << 16;  // ls_order_key16 << 16
+    if ((w * NSW + s) * 64 + lane >= cn) k = 0u;
+    key[s] = k;
+    m2 = max(m2, min(m1, k));
+    m1 = max(m1, k);
+  }
+  s_m[0][tid] = m1;
+  s_m[1][tid] = m2;
+  __syncthreads();
+  if (w == 0) {
+    uint32_t mm[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mm[2 * i] = s_m[0][64 * i + lane] >> 16;
+      mm[2 * i + 1] = s_m[1][64 * i + lane] >> 16;
+    }
+    const uint32_t lo = ls_kth_bisect<8>(mm, take, 0u, 15);
+    if (lane == 0) s_lo = lo;
+  }
+  __syncthreads();
+  const uint32_t lo = s_lo;
+  const uint32_t lo_sh = lo << 16;
+  int n = 0;  // this wave's keys >= lo
+#pragma unroll
+  for (int s = 0; s < NSW; ++s) n += __popcll(__ballot(lo != 0u && key[s] >= lo_sh));
+  if (lane == 0) s_cnt[w] = n;
+  __syncthreads();
+  int off = 0, total = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    off += i < w ? s_cnt[i] : 0;
+    total += s_cnt[i];
+  }
+  if (lo == 0u || total > 256) {  // no usable bound: the one-wave selection takes the row
+    if (w == 0) {
+      uint32_t* scr = s_scr;
+      ls_topk_select16<4 * NSW>(pooled, row * out_len, cn, take, 0, lane, orow, scr, id_max);
+    }
+    return;
+  }
+  int pos0 = off;
+#pragma unroll
+  for (int s = 0; s < NSW; ++s) {
+    const bool sv = key[s] >= lo_sh;
+    const uint64_t mk = __ballot(sv);
+    const int pos = (int)__builtin_amdgcn_mbcnt_hi(
+        (uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, (uint32_t)pos0));
+    if (sv) s_scr[pos] = key[s] | (uint32_t)((w * NSW + s) * 64 + lane);
+    pos0 += __popcll(mk);
+  }
+  __syncthreads();
+  if (w != 0) return;
+  uint32_t hi = 0u;  // this lane's maximum over the four waves (reduced inside)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hi = max(hi, s_m[0][64 * i + lane] >> 16);
+  if (total <= 64) return ls_topk_emit_packed<1>(s_scr, total, lo, hi, take, 0, lane, orow, id_max);
+  if (total <= 128) return ls_topk_emit_packed<2>(s_scr, total, lo, hi, take, 0, lane, orow, id_max);
+  return ls_topk_emit_packed<4>(s_scr, total, lo, hi, take, 0, lane, orow, id_max);
+}
+
 // ---------------------------------------------------------------------------
 // Split-K attention over the cache.  Workgroup (split s, row t, group g) has
 // four waves; wave w runs the pages of plan slots
@@ -859,6 +955,21 @@ extern "C" int ls_decode_select(const void* q, int64_t q_row_stride, const int32
   if (rc) return rc;
   // Rows of up to 8192 pages: one wave per row; longer rows: one workgroup
   // per row with the keys in LDS.
+  if (out_len > 256 && out_len <= 4 * 64 * 16 && take <= 128) {
+    // Four waves per row.
+    const dim3 gr((unsigned)((int64_t)num_kv_heads * total_q));
+    auto go = [&](auto nsw) {
+      hipLaunchKernelGGL((ls_decode_topk_wg_kernel<decltype(nsw)::value>), gr, dim3(256), 0, s,
+                         pooled, cu_seqlens_q, batch, total_q, num_kv_heads, cache_seqlens,
+                         (int)out_len, block_size, take, topk_idx);
+    };
+    const int nsw = (int)((out_len + 255) / 256);
+    if (nsw <= 2) go(std::integral_constant<int, 2>());
+    else if (nsw <= 4) go(std::integral_constant<int, 4>());
+    else if (nsw <= 8) go(std::integral_constant<int, 8>());
+    else go(std::integral_constant<int, 16>());
+    return ls_check_launch("ls_decode_topk_wg_kernel");
+  }
   if (out_len <= 8192) {
     const dim3 gw((unsigned)(((int64_t)num_kv_heads * total_q + 3) / 4));
     auto go = [&](auto kpl) {

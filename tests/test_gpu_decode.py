@@ -148,6 +148,27 @@ def test_decode_select_long_rows_match_oracle(lens, len_q):
                 assert kept == sorted(set(kept)) and row == kept + [-1] * (len(row) - len(kept))
 
 
+@pytest.mark.parametrize("lens", [[40000, 3000], [131072, 9000]])
+def test_decode_select_all_scores_tied(lens):
+    """Zero queries give every visible page the same stage-1 score: the top-k is
+    decided by the tie rule alone (lower pages first, after the forced ones), and
+    every key clears the lanes' bound, so the four-wave kernel hands the row to
+    the one-wave selection."""
+    cap = max(lens)
+    k, v, kc, kp, vp = _filled_cache(lens, cap, seed=7)
+    del k, v, kp, vp
+    B, H = len(lens), 32
+    cu_q = _cu([1] * B)
+    q = torch.zeros(B, H, D, dtype=torch.bfloat16)
+    ids = decode_topk_idx(q.to(DEV), kc, _i32(lens), _i32(cu_q), topk=64, local_blocks=4,
+                          init_blocks=1).cpu()
+    kc_packed = torch.cat([kc[b, :n_windows(L)].cpu() for b, L in enumerate(lens)])
+    cu_kc = _cu([n_windows(L) for L in lens])
+    want, pooled = oracle.decode_select(q, kc_packed, cu_q, cu_kc, lens, topk=64, local_blocks=4,
+                                        init_blocks=1, return_scores=True)
+    assert torch.equal(ids, want)
+
+
 def _packed(k, v, lens):
     return (torch.cat([k[b, :L].cpu() for b, L in enumerate(lens)]),
             torch.cat([v[b, :L].cpu() for b, L in enumerate(lens)]))
