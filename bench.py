@@ -662,7 +662,7 @@ def main() -> None:
 
     H, G, D = case.q.shape[1], case.k.shape[1], case.q.shape[2]
     locality = plan_locality(ids, cu_host)
-    secondary_plans = None
+    secondary_plans = secondary_unit = None
     if not nosa and not args.no_secondary:
         # The same layer on hidden states without planted topics: plans that
         # share few pages between neighbouring rows, like the whole-model
@@ -682,6 +682,23 @@ def main() -> None:
             "plan_locality": plan_locality(ids0, cu_host),
         }
         del c0, kc0, ids0
+        print("[bench] secondary: attention on unit-scale plants ...", file=sys.stderr, flush=True)
+        c1 = workloads.hidden_space_layer(wl["seq_lens"], device=dev, seed=0,
+                                          **workloads.UNIT_SCALE)
+        kc1, cu_c1 = compress_k(c1.k, cu, cu_seqlens_host=cu_host)
+        ids1 = leanselect_prefill_topk_idx(c1.q, kc1, cu, cu_c1, c1.selector, **kw)
+        ms1 = _event_ms(lambda: sparse_attention(c1.q, c1.k, c1.v, cu, cu, max_len, max_len, ids1), it)
+        fl1 = 4.0 * (H // G) * D * attention_keys(ids1, cu_host)
+        secondary_unit = {
+            "data": ("same shapes and seed, each planted row given one topic-amplitude vector "
+                     "(the unit vector of its plants' sum), so no page accumulates plants, and "
+                     "value projection std 0.4/sqrt(4096) (values of std ~0.5)"),
+            "attention_ms": round(ms1, 4),
+            "attention_tflops": round(fl1 / (ms1 * 1e-3) / 1e12, 2),
+            "frac": round(fl1 / (ms1 * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "plan_locality": plan_locality(ids1, cu_host),
+        }
+        del c1, kc1, ids1
     n_keys = attention_keys(ids, cu_host)
     attn_flops = 4.0 * (H // G) * D * n_keys
     sel_flops = selection_flops(case, all_pages=nosa)
@@ -702,9 +719,12 @@ def main() -> None:
         "data": ("synthetic: seeded hidden states X ~ N(0,1) [N, 4096] with rank-8 page topics "
                  "planted at amplitude 48 (each 64-token query block and 8 of its earlier pages "
                  "share a topic direction; the amplitude is this benchmark's choice, the "
-                 "reference fixes none), random-init projections (std 0.02); plan locality "
-                 "in config.plan_locality, and secondary.attention_without_topics for plans "
-                 "that share few pages"),
+                 "reference fixes none; a page chosen by several blocks accumulates their "
+                 "plants, up to ~56 on the earliest pages at 128K, so its keys and values "
+                 "grow with the count), random-init projections (std 0.02); plan locality "
+                 "in config.plan_locality, secondary.attention_without_topics for plans "
+                 "that share few pages and secondary.attention_unit_scale_plants for plants "
+                 "that do not accumulate"),
         "config": {
             "workload": args.workload,
             "seq_lens": list(wl["seq_lens"]),
@@ -733,6 +753,7 @@ def main() -> None:
             "select_tflops": round(sel_flops / (ms_select * 1e-3) / 1e12, 2),
             "select_flops": sel_flops,
             "attention_without_topics": secondary_plans,
+            "attention_unit_scale_plants": secondary_unit,
         },
     }
     if not args.no_cpu_baseline:

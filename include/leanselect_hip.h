@@ -253,8 +253,9 @@ int ls_sparse_attn_varlen(const void* q, int64_t q_row_stride, const void* k,
  * allocating library routine); a request whose workspace would exceed the
  * array (ls_sparse_attn_workspace_size > 64 MiB, about 65000 keys at 2 KV
  * heads) fails with LS_ERR_UNSUPPORTED before any device work.  `status`
- * (optional, device int32) receives the status word described above; without
- * it the word stays in the array.  Every call on one GPU shares that GPU's
+ * (optional, device int32) receives the status word described above (0 for a
+ * call with no query row or no sequence, written by a one-thread kernel);
+ * without it the word stays in the array.  Every call on one GPU shares that GPU's
  * array, so calls that overlap on one GPU (concurrent streams or host threads)
  * race and must be serialised by the caller.
  */
@@ -526,6 +527,31 @@ int ls_decode_select(const void* q, int64_t q_row_stride, const int32_t* cu_seql
                      int32_t kernel_size, int32_t kernel_stride, int32_t init_blocks,
                      int32_t local_blocks, int64_t out_len, int32_t take, int32_t* topk_idx,
                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Stage-1 scores of packed query rows over packed compressed keys, without a
+ * causal limit (the decode form):
+ *   out[g, t, j] = sum over the heads h of group g of softmax_j(scale * q[t, h]
+ *                  . kc[cu_seqlens_kc[b] + j, g])   for j < n_c(b),
+ * n_c(b) = min(cu_seqlens_kc[b + 1] - cu_seqlens_kc[b], max_kc) for the row's
+ * sequence b; 0 for j >= n_c(b) and where the score is NaN.  Rounded to the
+ * query dtype.  q [total_q, H, D] (rows q_row_stride apart), kc [total_kc, G,
+ * D] (rows kc_row_stride apart), out [G, total_q, out_cols] contiguous.
+ * head_dim 128, at most 16 query heads per KV head, bf16 or fp16.  Workspace
+ * from ls_stage1_scores_workspace_size.
+ * Replaces infllmv2_attn_stage1(q, k, v, cu_seqlens_q=, cu_seqlens_k=,
+ * cu_seqlens_v=, max_seqlen_q=, max_seqlen_k=, causal=False)
+ * (third_party/infllmv2/paper1.patch:2312-2361, NaN -> 0 at 2359), which
+ * compressed_attention calls when decoding (leanselect/models/minicpm.py:
+ * 673-683).
+ */
+size_t ls_stage1_scores_workspace_size(int64_t total_q, int32_t num_kv_heads, int64_t max_kc);
+int ls_stage1_scores(const void* q, int64_t q_row_stride, const int32_t* cu_seqlens_q,
+                     int64_t total_q, const void* kc, int64_t kc_row_stride,
+                     const int32_t* cu_seqlens_kc, int32_t batch, int64_t max_kc,
+                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                     float softmax_scale, void* out, int64_t out_cols, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 /*
  * Block-sparse attention of packed query rows over the cache: row i of

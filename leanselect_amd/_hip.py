@@ -6,6 +6,7 @@ when it is missing: there is no fallback implementation.
 from __future__ import annotations
 
 import ctypes
+from collections import deque
 from pathlib import Path
 
 import torch
@@ -88,6 +89,10 @@ SIGNATURES = {
     "ls_decode_select": (
         _i32, [_p, _i64, _p, _i64, _p, _i64, _i64, _p, _i32, _i64, _i32, _i32, _i32, _i32, _f32,
                _i32, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _p, _p, _sz, _p]),
+    "ls_stage1_scores_workspace_size": (_sz, [_i64, _i32, _i64]),
+    "ls_stage1_scores": (
+        _i32, [_p, _i64, _p, _i64, _p, _i64, _p, _i32, _i64, _i32, _i32, _i32, _i32, _f32, _p,
+               _i64, _p, _sz, _p]),
     "ls_sparse_attn_kvcache_workspace_size": (_sz, [_i64, _i32, _i32]),
     "ls_sparse_attn_kvcache": (
         _i32, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p,
@@ -175,19 +180,77 @@ def check_out(out: torch.Tensor, shape: tuple, dtype: torch.dtype, device: torch
     return out
 
 
-def check_attn_status(ws: torch.Tensor, name: str) -> None:
-    """Read an attention workspace's status word (its first 4 bytes) once the
-    call's kernels have finished, and raise if a wave's wait for a staged page
-    expired.  This waits for the stream.  Under graph capture the word cannot
-    be read; the call is then not checked here, and a replay whose wait expired
-    shows it in its output instead (the rows of such a wave are NaN)."""
-    if torch.cuda.is_current_stream_capturing():
-        return
-    status = int(ws[:4].view(torch.int32).item())
+class _StatusQueue:
+    """Attention status words read without stalling the host.
+
+    Each eager attention call queues a non-blocking copy of its workspace's
+    status word into pinned host memory, followed by an event; the word is
+    inspected once that event has completed -- at a later call's poll, or at
+    ``attn_status_sync``.  So no call waits for its own kernels, and a wait that
+    expired is reported by the first poll that finds the copy done."""
+
+    MAX_PENDING = 64
+
+    def __init__(self) -> None:
+        self.pending: deque = deque()
+
+    def push(self, ws: torch.Tensor, name: str) -> None:
+        host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        host.copy_(ws[:4].view(torch.int32), non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(ws.device))
+        self.pending.append((ev, host, name))
+
+    def poll(self, block: bool = False) -> None:
+        while self.pending:
+            ev, host, name = self.pending[0]
+            if not block and len(self.pending) <= self.MAX_PENDING and not ev.query():
+                return
+            ev.synchronize()
+            self.pending.popleft()
+            _raise_for_status(int(host[0]), name)
+
+
+_status_queue = _StatusQueue()
+
+
+def _raise_for_status(status: int, name: str) -> None:
     if status & LS_ATTN_RING_TIMEOUT:
         raise RuntimeError(f"{name}: a wait for a staged K/V page expired; the output is invalid")
     if status:
         raise RuntimeError(f"{name}: unknown status {status:#x}")
+
+
+def check_attn_status(ws: torch.Tensor, name: str, *, sync: bool = False) -> None:
+    """Check an attention call's status word (the first 4 bytes of its workspace).
+
+    By default the word is queued for a deferred, non-blocking check (see
+    ``_StatusQueue``): earlier calls whose copies have landed are checked now,
+    and this call is checked by a later poll.  With ``sync=True`` the host waits
+    for the stream and raises at once if this call's wait for a staged page
+    expired.  Under graph capture the word cannot be read; the call is then not
+    checked here, and a replay whose wait expired shows it in its output instead
+    (the rows of such a wave are NaN)."""
+    if torch.cuda.is_current_stream_capturing():
+        return
+    if sync:
+        _status_queue.poll(block=True)
+        _raise_for_status(int(ws[:4].view(torch.int32).item()), name)
+        return
+    _status_queue.push(ws, name)
+    _status_queue.poll(block=False)
+
+
+def attn_status_sync() -> None:
+    """Wait for every queued attention status word and raise for the first
+    call whose wait for a staged K/V page expired."""
+    _status_queue.poll(block=True)
+
+
+def poll_attn_status() -> None:
+    """Check the queued status words whose copies have landed (never waits)."""
+    if not torch.cuda.is_current_stream_capturing():
+        _status_queue.poll(block=False)
 
 
 def stream_of(device: torch.device) -> int:

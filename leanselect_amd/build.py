@@ -36,8 +36,10 @@ HIPCC_FLAGS = [
 FILE_FLAGS = {
     "ls_attention": ["-mno-amdgpu-ieee", "-fno-honor-nans"],
     # MFMAs accumulate in ordinary VGPRs, so their results need no copies out
-    # of the accumulation registers before the pooling reads them.
-    "ls_select": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mno-amdgpu-ieee", "-fno-honor-nans"],
+    # of the accumulation registers before the pooling reads them.  NaN is
+    # honoured here: page maxima propagate NaN (v_maximum3_f32), as the
+    # reference's max pooling does.
+    "ls_select": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     # The decoder kernels round every float32 product and sum separately, as
     # the reference's torch expressions do.
     "ls_model": ["-ffp-contract=off"],

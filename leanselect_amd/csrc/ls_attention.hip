@@ -80,6 +80,12 @@ __global__ void ls_attn_plan_kernel(const int32_t* __restrict__ cu_q,
   }
 }
 
+// Writes 0 to a caller's status word (a kernel rather than a memset, so that
+// the call stays safe to capture in a graph).
+__global__ void ls_attn_status_clear_kernel(int32_t* __restrict__ status) {
+  if (LS_BID_X == 0 && LS_TID == 0) *status = 0;
+}
+
 // ---------------------------------------------------------------------------
 // Tile kernel: one workgroup = LS_ATT_TILE (16) consecutive query rows of one
 // sequence and one KV group for 16 of its query heads (8 waves x 2 rows, two
@@ -962,7 +968,13 @@ extern "C" int ls_sparse_attn_varlen_noalloc(
              "%zu bytes of scratch, above the static %u (use ls_sparse_attn_varlen with a "
              "workspace)",
              (long long)total_k, batch, num_kv_heads, need, LS_NOALLOC_SCRATCH_BYTES);
-  if (total_q == 0 || batch == 0) return LS_OK;
+  if (total_q == 0 || batch == 0) {
+    // Nothing to attend; the caller's status word still gets this call's value.
+    if (!status) return LS_OK;
+    hipLaunchKernelGGL(ls_attn_status_clear_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
+                       status);
+    return ls_check_launch("ls_attn_status_clear_kernel");
+  }
   void* ws = nullptr;
   const int rc = scratch_for_stream((hipStream_t)stream, &ws);
   if (rc) return rc;

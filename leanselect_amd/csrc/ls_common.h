@@ -105,6 +105,19 @@ __device__ __forceinline__ float ls_shfl_xor(float v, int mask) {
   return __shfl_xor(v, mask, LS_WAVE);
 }
 
+// NaN-propagating maximum (v_maximum3_f32 on gfx950), as torch's amax and
+// max_pool1d propagate NaN.  Only meaningful where NaN is honoured (files
+// built without -fno-honor-nans).
+__device__ __forceinline__ float ls_fmax_nan(float a, float b) {
+  return __builtin_elementwise_maximum(a, b);
+}
+
+// NaN of either sign becomes the positive canonical quiet NaN, whose order key
+// lies above +inf's (torch.topk ranks every NaN above +inf).
+__device__ __forceinline__ float ls_canon_nan(float x) {
+  return __builtin_isnan(x) ? __builtin_nanf("") : x;
+}
+
 // Order-preserving unsigned keys of 16-bit (bf16 / fp16) and float32 scores:
 // a > b as floats  <=>  key(a) > key(b) as integers (NaN aside).
 __host__ __device__ __forceinline__ uint32_t ls_order_key16(uint16_t b) {

@@ -142,7 +142,11 @@ __device__ __forceinline__ int ls_dec_n_c(int64_t len, int ks, int stride, int64
 }
 
 // x[g][t][h][j] (float, base-2 units, -inf past n_c), part[g][t][c][h] = (max, sum).
-template <int DT>
+// Cache form (VARLEN false): sequence b's compressed keys are rows
+// kcc[b kbs + j krs] and n_c(b) follows from its token count lens[b].  Packed
+// form (VARLEN true): they are rows kcc[(lens[b] + j) krs] with n_c(b) =
+// lens[b + 1] - lens[b] (lens = cu_seqlens of the compressed keys).
+template <int DT, bool VARLEN = false>
 __global__ __launch_bounds__(64) void ls_stage1_chunk_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, const int32_t* __restrict__ cu_q, int batch,
     int64_t total_q, const uint16_t* __restrict__ kcc, int64_t kbs, int64_t krs,
@@ -154,7 +158,9 @@ __global__ __launch_bounds__(64) void ls_stage1_chunk_kernel(
   const int g = LS_BID_Z;
   const int lane = LS_TID, r = lane & 15, qg = lane >> 4;
   const int b = ls_find_segment(cu_q, batch, t);
-  const int nc = ls_dec_n_c(cache_seqlens[b], ks, stride, max_kc);
+  const int nc = VARLEN ? (int)min((int64_t)(cache_seqlens[b + 1] - cache_seqlens[b]), max_kc)
+                        : ls_dec_n_c(cache_seqlens[b], ks, stride, max_kc);
+  const int64_t kbase = VARLEN ? (int64_t)cache_seqlens[b] * krs : (int64_t)b * kbs;
   float* xrow = x + ((int64_t)g * total_q + t) * 16 * ncpad;
   float* prow = part + (((int64_t)g * total_q + t) * n_chunks + c) * 32;
   // Q^T fragments (B operand): lane (r, qg) holds head r, dims 32 ks + 8 qg + 0..7.
@@ -171,7 +177,7 @@ __global__ __launch_bounds__(64) void ls_stage1_chunk_kernel(
     const int j = 64 * c + 16 * kb + r;  // key row of this lane's A fragment
     ls_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     const bool key_ok = j < nc;
-    const uint16_t* krow = kcc + (int64_t)b * kbs + (int64_t)j * krs + (int64_t)g * D + 8 * qg;
+    const uint16_t* krow = kcc + kbase + (int64_t)j * krs + (int64_t)g * D + 8 * qg;
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4) {
       const ls_u32x4 kf = key_ok ? ls_load16(krow + 32 * k4) : ls_u32x4{0u, 0u, 0u, 0u};
@@ -207,6 +213,50 @@ __global__ __launch_bounds__(64) void ls_stage1_chunk_kernel(
   }
 }
 
+// Each head's log2-sum-exp of one (row, group) from its nch chunk partials
+// prow[c * 32 + 2 h] = (max, sum), into s_lse[h] for h < gs, by the 256
+// threads of a workgroup (every thread calls it): sixteen consecutive threads
+// per head (four heads per wave) reduce the head's partials, each a strided
+// share, then butterfly shuffles.
+__device__ __forceinline__ void ls_stage1_lse(const float* __restrict__ prow, int nch, int gs,
+                                              int tid, float* __restrict__ s_lse) {
+  const int h = tid >> 4, share = tid & 15;
+  // A thread's first eight (max, sum) pairs (chunks share + 16 i: all of
+  // them up to 128 chunks) are loaded once, together, and kept for the sum;
+  // chunks beyond are read in the loops.
+  constexpr int NP = 8;
+  float pm[NP], pl[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int c = share + 16 * i;
+    const bool ok = h < gs && c < nch;
+    const float2 v = ok ? *reinterpret_cast<const float2*>(prow + c * 32 + 2 * h)
+                        : make_float2(-INFINITY, 0.f);
+    pm[i] = v.x;
+    pl[i] = v.y;
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) M = fmaxf(M, pm[i]);
+  if (h < gs)
+    for (int c = share + 16 * NP; c < nch; c += 16) M = fmaxf(M, prow[c * 32 + 2 * h]);
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) M = fmaxf(M, ls_shfl_xor(M, o));
+  float L = 0.f;
+  if (h < gs && M != -INFINITY) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i)
+      if (pm[i] != -INFINITY) L += pl[i] * __builtin_amdgcn_exp2f(pm[i] - M);
+    for (int c = share + 16 * NP; c < nch; c += 16) {
+      const float mc = prow[c * 32 + 2 * h];
+      if (mc != -INFINITY) L += prow[c * 32 + 2 * h + 1] * __builtin_amdgcn_exp2f(mc - M);
+    }
+  }
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) L += ls_shfl_xor(L, o);
+  if (h < gs && share == 0) s_lse[h] = M + __log2f(L);
+}
+
 // Pass 2 and the page max-pool of max_pooling_1d_varlen, fused.  Workgroup
 // (page block pb, row t, group g) covers pages [ppb pb, ppb pb + ppb) of
 // sp = block_size / kernel_stride keys each (ppb sp <= 256).  It forms each
@@ -235,47 +285,9 @@ __global__ __launch_bounds__(256) void ls_stage1_pool_kernel(
   const int64_t j0 = p0 * sp - 1;  // key of LDS slot 0
   const int n_keys = ppb * sp + 1;
   const bool has_keys = max((int64_t)0, j0) < (int64_t)nc;  // uniform
-  if (has_keys) {
-    // Sixteen consecutive threads per head (four heads per wave) reduce the
-    // head's chunk partials: each a strided share, then butterfly shuffles.
-    const float* prow = part + ((int64_t)g * total_q + t) * n_chunks * 32;
-    const int nch = (nc + 63) / 64;
-    const int h = tid >> 4, share = tid & 15;
-    // A thread's first eight (max, sum) pairs (chunks share + 16 i: all of
-    // them up to 128 chunks) are loaded once, together, and kept for the sum;
-    // chunks beyond are read in the loops.
-    constexpr int NP = 8;
-    float pm[NP], pl[NP];
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int c = share + 16 * i;
-      const bool ok = h < gs && c < nch;
-      const float2 v = ok ? *reinterpret_cast<const float2*>(prow + c * 32 + 2 * h)
-                          : make_float2(-INFINITY, 0.f);
-      pm[i] = v.x;
-      pl[i] = v.y;
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < NP; ++i) M = fmaxf(M, pm[i]);
-    if (h < gs)
-      for (int c = share + 16 * NP; c < nch; c += 16) M = fmaxf(M, prow[c * 32 + 2 * h]);
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) M = fmaxf(M, ls_shfl_xor(M, o));
-    float L = 0.f;
-    if (h < gs && M != -INFINITY) {
-#pragma unroll
-      for (int i = 0; i < NP; ++i)
-        if (pm[i] != -INFINITY) L += pl[i] * __builtin_amdgcn_exp2f(pm[i] - M);
-      for (int c = share + 16 * NP; c < nch; c += 16) {
-        const float mc = prow[c * 32 + 2 * h];
-        if (mc != -INFINITY) L += prow[c * 32 + 2 * h + 1] * __builtin_amdgcn_exp2f(mc - M);
-      }
-    }
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) L += ls_shfl_xor(L, o);
-    if (h < gs && share == 0) s_lse[h] = M + __log2f(L);
-  }
+  if (has_keys)
+    ls_stage1_lse(part + ((int64_t)g * total_q + t) * n_chunks * 32, (nc + 63) / 64, gs, tid,
+                  s_lse);
   __syncthreads();
   const float* xrow = x + ((int64_t)g * total_q + t) * 16 * ncpad;
   for (int i = tid; i < n_keys; i += 256) {
@@ -308,6 +320,40 @@ __global__ __launch_bounds__(256) void ls_stage1_pool_kernel(
       for (int e = 0; e <= sp; ++e) v = fmaxf(v, s_sc[i * sp + e]);
     }
     orow[p] = ls_f32_to_bf16(v);
+  }
+}
+
+// Stage-1 scores as infllmv2_attn_stage1 returns them when decoding
+// (paper1.patch:2312-2361 with causal=False): out[g][t][j] = sum over the
+// group's heads of softmax_j(scale q[t][h] . kc[j][g]) for the n_c(b)
+// compressed keys of the row's sequence, rounded to the query dtype, 0 for
+// j >= n_c(b) and where the score is NaN.  One workgroup per (row, group).
+template <int DT>
+__global__ __launch_bounds__(256) void ls_stage1_scores_kernel(
+    const float* __restrict__ x, const float* __restrict__ part, const int32_t* __restrict__ cu_q,
+    int batch, int64_t total_q, const int32_t* __restrict__ cu_kc, int64_t max_kc, int gs,
+    int64_t ncpad, int n_chunks, int64_t out_cols, uint16_t* __restrict__ out) {
+  const int64_t t = LS_BID_X;
+  const int g = LS_BID_Y;
+  const int tid = LS_TID;
+  __shared__ float s_lse[16];
+  const int b = ls_find_segment(cu_q, batch, t);
+  const int nc = (int)min((int64_t)(cu_kc[b + 1] - cu_kc[b]), max_kc);
+  if (nc > 0)
+    ls_stage1_lse(part + ((int64_t)g * total_q + t) * n_chunks * 32, (nc + 63) / 64, gs, tid,
+                  s_lse);
+  __syncthreads();
+  const float* xrow = x + ((int64_t)g * total_q + t) * 16 * ncpad;
+  uint16_t* orow = out + ((int64_t)g * total_q + t) * out_cols;
+  for (int64_t j = tid; j < out_cols; j += 256) {
+    float v = 0.f;
+    if (j < nc) {
+      float sum = 0.f;
+      for (int h = 0; h < gs; ++h) sum += __builtin_amdgcn_exp2f(xrow[(int64_t)h * ncpad + j] - s_lse[h]);
+      v = sum;
+    }
+    const uint16_t o = LsElem<DT>::from_f(v);
+    orow[j] = (__builtin_isnan(v) ? (uint16_t)0 : o);
   }
 }
 
@@ -536,9 +582,9 @@ __global__ __launch_bounds__(256) void ls_decode_topk_wg_kernel(
   uint32_t hi = 0u;  // this lane's maximum over the four waves (reduced inside)
 #pragma unroll
   for (int i = 0; i < 4; ++i) hi = max(hi, s_m[0][64 * i + lane] >> 16);
-  if (total <= 64) return ls_topk_emit_packed<1>(s_scr, total, lo, hi, take, 0, lane, orow, id_max);
-  if (total <= 128) return ls_topk_emit_packed<2>(s_scr, total, lo, hi, take, 0, lane, orow, id_max);
-  return ls_topk_emit_packed<4>(s_scr, total, lo, hi, take, 0, lane, orow, id_max);
+  if (total <= 64) ls_topk_emit_packed<1>(s_scr, total, lo, hi, take, 0, lane, orow, id_max);
+  else if (total <= 128) ls_topk_emit_packed<2>(s_scr, total, lo, hi, take, 0, lane, orow, id_max);
+  else ls_topk_emit_packed<4>(s_scr, total, lo, hi, take, 0, lane, orow, id_max);
 }
 
 // ---------------------------------------------------------------------------
@@ -1061,4 +1107,65 @@ extern "C" int ls_sparse_attn_kvcache(const void* q, int64_t q_row_stride,
                        gs, head_dim, splits, (uint16_t*)out, softmax_lse);
   }
   return ls_check_launch("ls_decode_combine_kernel");
+}
+
+extern "C" size_t ls_stage1_scores_workspace_size(int64_t total_q, int32_t num_kv_heads,
+                                                  int64_t max_kc) {
+  return sel_ws(total_q, num_kv_heads, max_kc, 0).total;
+}
+
+extern "C" int ls_stage1_scores(const void* q, int64_t q_row_stride, const int32_t* cu_seqlens_q,
+                                int64_t total_q, const void* kc, int64_t kc_row_stride,
+                                const int32_t* cu_seqlens_kc, int32_t batch, int64_t max_kc,
+                                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                int32_t dtype, float softmax_scale, void* out, int64_t out_cols,
+                                void* ws, size_t ws_bytes, void* stream) {
+  LS_REQUIRE(batch > 0 && total_q >= 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
+                 max_kc >= 0 && out_cols >= 0,
+             LS_ERR_INVALID, "ls_stage1_scores: bad sizes");
+  const int gs = num_heads / num_kv_heads;
+  LS_REQUIRE(head_dim == 128 && gs >= 1 && gs <= 16, LS_ERR_UNSUPPORTED,
+             "ls_stage1_scores: head_dim 128 and at most 16 query heads per KV head");
+  LS_REQUIRE(dtype == LS_BF16 || dtype == LS_F16, LS_ERR_UNSUPPORTED,
+             "ls_stage1_scores: bf16 or fp16 queries");
+  LS_REQUIRE(total_q <= 0x7fffffffLL && num_kv_heads <= 65535, LS_ERR_INVALID,
+             "ls_stage1_scores: bad sizes");
+  LS_REQUIRE(q_row_stride % 8 == 0 && kc_row_stride % 8 == 0, LS_ERR_UNSUPPORTED,
+             "ls_stage1_scores: query and key rows must be 16-byte aligned");
+  if (total_q == 0 || out_cols == 0) return LS_OK;
+  LS_REQUIRE(q && cu_seqlens_q && cu_seqlens_kc && out && ws && (max_kc == 0 || kc),
+             LS_ERR_INVALID, "ls_stage1_scores: null pointer");
+  const SelWs L = sel_ws(total_q, num_kv_heads, max_kc, 0);
+  LS_REQUIRE(ws_bytes >= L.total, LS_ERR_WORKSPACE, "ls_stage1_scores: workspace %zu < %zu",
+             ws_bytes, L.total);
+  uint8_t* w = (uint8_t*)ws;
+  float* x = (float*)(w + L.x);
+  float* part = (float*)(w + L.part);
+  hipStream_t s = (hipStream_t)stream;
+  const float scale_log2 = softmax_scale * 1.4426950408889634f;
+  int rc;
+  if (max_kc > 0) {
+    const dim3 g1((unsigned)L.n_chunks, (unsigned)total_q, num_kv_heads);
+    if (dtype == LS_BF16)
+      hipLaunchKernelGGL((ls_stage1_chunk_kernel<LS_BF16, true>), g1, dim3(64), 0, s,
+                         (const uint16_t*)q, q_row_stride, cu_seqlens_q, batch, total_q,
+                         (const uint16_t*)kc, (int64_t)0, kc_row_stride, cu_seqlens_kc, 0, 1,
+                         max_kc, gs, head_dim, scale_log2, L.ncpad, L.n_chunks, x, part);
+    else
+      hipLaunchKernelGGL((ls_stage1_chunk_kernel<LS_F16, true>), g1, dim3(64), 0, s,
+                         (const uint16_t*)q, q_row_stride, cu_seqlens_q, batch, total_q,
+                         (const uint16_t*)kc, (int64_t)0, kc_row_stride, cu_seqlens_kc, 0, 1,
+                         max_kc, gs, head_dim, scale_log2, L.ncpad, L.n_chunks, x, part);
+    if ((rc = ls_check_launch("ls_stage1_chunk_kernel"))) return rc;
+  }
+  const dim3 g2((unsigned)total_q, num_kv_heads);
+  if (dtype == LS_BF16)
+    hipLaunchKernelGGL(ls_stage1_scores_kernel<LS_BF16>, g2, dim3(256), 0, s, x, part,
+                       cu_seqlens_q, batch, total_q, cu_seqlens_kc, max_kc, gs, L.ncpad,
+                       L.n_chunks, out_cols, (uint16_t*)out);
+  else
+    hipLaunchKernelGGL(ls_stage1_scores_kernel<LS_F16>, g2, dim3(256), 0, s, x, part,
+                       cu_seqlens_q, batch, total_q, cu_seqlens_kc, max_kc, gs, L.ncpad,
+                       L.n_chunks, out_cols, (uint16_t*)out);
+  return ls_check_launch("ls_stage1_scores_kernel");
 }

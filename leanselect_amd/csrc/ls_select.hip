@@ -549,10 +549,10 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_mfma_kernel(
     for (int tb = 0; tb < 4; ++tb) rot[tb] = ls_shfl(acc[tb][3], (lane - 16) & 63);
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
-      const float m4 = fmaxf(fmaxf(acc[tb][0], acc[tb][1]), fmaxf(acc[tb][2], acc[tb][3]));
+      const float m4 = ls_fmax_nan(ls_fmax_nan(acc[tb][0], acc[tb][1]), ls_fmax_nan(acc[tb][2], acc[tb][3]));
       const float prev = q == 0 ? carry[tb] : rot[tb];
       carry[tb] = rot[tb];
-      so[(16 * tb + r) * SP + 4 * (j & 15) + q] = LsElem<DT>::from_f(fmaxf(m4, prev));
+      so[(16 * tb + r) * SP + 4 * (j & 15) + q] = LsElem<DT>::from_f(ls_canon_nan(ls_fmax_nan(m4, prev)));
     }
     if ((j & 15) == 15 || j == jw_hi) flush(j >> 4);
   };
@@ -739,10 +739,10 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_panel_kernel(
     for (int tb = 0; tb < 4; ++tb) rot[tb] = ls_shfl(acc[tb][3], (lane - 16) & 63);
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
-      const float m4 = fmaxf(fmaxf(acc[tb][0], acc[tb][1]), fmaxf(acc[tb][2], acc[tb][3]));
+      const float m4 = ls_fmax_nan(ls_fmax_nan(acc[tb][0], acc[tb][1]), ls_fmax_nan(acc[tb][2], acc[tb][3]));
       const float prev = q == 0 ? carry[tb] : rot[tb];
       carry[tb] = rot[tb];
-      so[(16 * tb + r) * SP + 4 * (j & 15) + q] = LsElem<DT>::from_f(fmaxf(m4, prev));
+      so[(16 * tb + r) * SP + 4 * (j & 15) + q] = LsElem<DT>::from_f(ls_canon_nan(ls_fmax_nan(m4, prev)));
     }
   };
 
@@ -811,17 +811,45 @@ __global__ __launch_bounds__(256) void ls_score_f32_kernel(
     const float* krow = kt + ((int64_t)g * Na + a0 + a) * F;
     float acc = 0.f;
     for (int f = 0; f < F; ++f) acc = fmaf(qrow[f], krow[f], acc);
-    best = fmaxf(best, acc);
+    best = ls_fmax_nan(best, acc);
   }
-  out[((int64_t)g * Nq + t) * out_stride + p] = best;
+  out[((int64_t)g * Nq + t) * out_stride + p] = ls_canon_nan(best);
 }
 
 
+// Number of NaN keys (keys above rule.hi) among the cn candidate scores at
+// P[base ..] of one row; every lane of the wave calls it and gets the count.
+template <bool KEY32>
+__device__ __forceinline__ int ls_count_nan_keys(const void* __restrict__ P, int64_t base, int cn,
+                                                 int lane, const LsInvalidKeys& rule) {
+  int n = 0;
+  for (int c0 = 0; c0 < cn; c0 += 64) {
+    const int c = c0 + lane;
+    uint32_t k = 0u;
+    if (c < cn) {
+      if constexpr (KEY32) k = ls_order_key32(((const uint32_t*)P)[base + c]);
+      else k = ls_order_key16(((const uint16_t*)P)[base + c]);
+    }
+    n += __popcll(__ballot(k > rule.hi));
+  }
+  return n;
+}
+
+// Selection of one row in the reference's order (minicpm.py:3124-3141): the
+// visible pages are ranked by score with the forced pages at +inf, and
+// torch.topk ranks NaN above +inf; the chosen pages with a NaN or -inf score
+// become -1.  Rows therefore normally hold the forced pages (sink pages, then
+// the local window) plus the top kk of the other visible pages, written in
+// page order; NaN scores (canonical, keys above rule.hi) displace forced pages
+// only when there are more of them than kk, in which case the forced pages
+// keep the slots left after the NaN ones (the lowest forced pages first, as
+// the ties at +inf resolve to the lower page) and the others become -1.
 template <int KPL, bool KEY32>
 __global__ __launch_bounds__(256) void ls_topk_kernel(
     const void* __restrict__ P, int64_t p_stride, const int32_t* __restrict__ cu_q,
     const int32_t* __restrict__ cu_a, int batch, int64_t total_q, int G, int take,
-    int init_blocks, int local_blocks, int block_size, int32_t* __restrict__ topk_idx) {
+    int init_blocks, int local_blocks, int block_size, LsInvalidKeys rule,
+    int32_t* __restrict__ topk_idx) {
   __shared__ uint32_t s_scr[4][320];  // per-wave gather space of the k-th key search
   const int lane = threadIdx.x & 63;
   // The wave index is uniform: keep the row and everything derived from it scalar.
@@ -847,14 +875,20 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
   const int lo_end = min(init_blocks, qp + 1);
   const int hi_start = max(qp - local_blocks, lo_end);
   const int n_forced = lo_end + (qp + 1 - hi_start);
+  // (Clamped to the row's columns, as the scoring is.)
+  const int cn = (int)max((int64_t)0, min((int64_t)(hi_start - lo_end), p_stride - lo_end));
+  const int64_t base = row * p_stride + lo_end;
   for (int i = n_valid + lane; i < take; i += 64) orow[i] = -1;
   if (n_forced >= n_valid) {
-    for (int i = lane; i < n_valid; i += 64) orow[i] = i < lo_end ? i : hi_start + (i - lo_end);
+    // The budget holds forced pages only: the first n_valid of them in page
+    // order, after any NaN-scored other pages (emitted as -1).
+    const int n_nan = cn > 0 ? ls_count_nan_keys<KEY32>(P, base, cn, lane, rule) : 0;
+    const int n_keep = max(0, n_valid - n_nan);
+    for (int i = lane; i < n_valid; i += 64)
+      orow[i] = i >= n_keep ? -1 : (i < lo_end ? i : hi_start + (i - lo_end));
     return;
   }
   const int kk = n_valid - n_forced;
-  // (Clamped to the row's columns, as the scoring is.)
-  const int cn = (int)min((int64_t)(hi_start - lo_end), p_stride - lo_end);
 
   for (int i = lane; i < lo_end; i += 64) orow[i] = i;
   const int hi_pos = lo_end + kk;
@@ -862,19 +896,39 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
 
   // Candidates in registers, NS slots of 64; the row's slot count is uniform,
   // so the branch picks one straight-line body per wave.
-  const int64_t base = row * p_stride + lo_end;
-  if constexpr (!KEY32) {
-    return ls_topk_select16<KPL>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
-  } else {
-    const int n_slots = (cn + 63) >> 6;
-    if (n_slots <= 1) return ls_topk_row<1, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
-    if (n_slots <= 2) return ls_topk_row<2, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
-    if (n_slots <= 4 || KPL <= 4) return ls_topk_row<(KPL < 4 ? KPL : 4), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
-    if (n_slots <= 8 || KPL <= 8) return ls_topk_row<(KPL < 8 ? KPL : 8), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
-    if (n_slots <= 16 || KPL <= 16) return ls_topk_row<(KPL < 16 ? KPL : 16), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
-    if (n_slots <= 32 || KPL <= 32) return ls_topk_row<(KPL < 32 ? KPL : 32), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
-    if (n_slots <= 64 || KPL <= 64) return ls_topk_row<(KPL < 64 ? KPL : 64), KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
-    return ls_topk_row<KPL, KEY32>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX);
+  auto select = [&]() -> uint32_t {
+    if constexpr (!KEY32) {
+      return ls_topk_select16<KPL>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX, rule);
+    } else {
+      const int n_slots = (cn + 63) >> 6;
+#define LS_TOPK32_CASE(N)                                                                      \
+      if (n_slots <= (N) || KPL <= (N))                                                        \
+        return ls_topk_row<(KPL < (N) ? KPL : (N)), true>(P, base, cn, kk, lo_end, lane, orow, \
+                                                          scr, INT32_MAX, rule);
+      LS_TOPK32_CASE(1)
+      LS_TOPK32_CASE(2)
+      LS_TOPK32_CASE(4)
+      LS_TOPK32_CASE(8)
+      LS_TOPK32_CASE(16)
+      LS_TOPK32_CASE(32)
+      LS_TOPK32_CASE(64)
+#undef LS_TOPK32_CASE
+      return ls_topk_row<KPL, true>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX, rule);
+    }
+  };
+  const uint32_t T = select();
+  if (T > rule.hi) {
+    // The kk-th key is NaN: kk or more NaN-scored pages, all chosen (as -1).
+    // Beyond kk of them they displace forced pages from the end of the page
+    // order.  (Rare; the forced pages written above are rewritten once their
+    // stores have completed.)
+    const int n_nan = ls_count_nan_keys<KEY32>(P, base, cn, lane, rule);
+    const int n_keep = max(0, n_valid - n_nan);
+    if (n_keep < n_forced) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      for (int f = n_keep + lane; f < n_forced; f += 64)
+        orow[f < lo_end ? f : hi_pos + (f - lo_end)] = -1;
+    }
   }
 }
 
@@ -1077,28 +1131,44 @@ int score(int dtype, int F, const void* qt, int64_t Nq, const void* kt, int64_t 
                                         out_stride);
 }
 
+// The invalid-key rule of the prefill selection for score dtype dt: canonical
+// NaN keys lie above +inf's key, and -inf's key marks -inf.
+LsInvalidKeys prefill_rule(int dt) {
+  LsInvalidKeys r;
+  if (dt == LS_F32) {
+    r.hi = ls_order_key32(0x7f800000u);
+    r.ninf = ls_order_key32(0xff800000u);
+  } else {
+    r.hi = ls_order_key16(dt == LS_BF16 ? 0x7f80u : 0x7c00u);
+    r.ninf = ls_order_key16(dt == LS_BF16 ? 0xff80u : 0xfc00u);
+  }
+  return r;
+}
+
 template <int KPL, bool KEY32>
 void launch_topk_kpl(dim3 grid, hipStream_t s, const void* P, int64_t ps, const int32_t* cu_q,
                      const int32_t* cu_a, int batch, int64_t total_q, int G, int take, int init,
-                     int local, int bs, int32_t* out) {
+                     int local, int bs, int dt, int32_t* out) {
   hipLaunchKernelGGL((ls_topk_kernel<KPL, KEY32>), grid, dim3(256), 0, s, P, ps, cu_q, cu_a,
-                     batch, total_q, G, take, init, local, bs, out);
+                     batch, total_q, G, take, init, local, bs, prefill_rule(dt), out);
 }
 
 template <bool KEY32>
 int launch_topk(int max_pages, dim3 grid, hipStream_t s, const void* P, int64_t ps,
                 const int32_t* cu_q, const int32_t* cu_a, int batch, int64_t total_q, int G,
-                int take, int init, int local, int bs, int32_t* out) {
+                int take, int init, int local, int bs, int dt, int32_t* out) {
+#define LS_TOPK_ARGS grid, s, P, ps, cu_q, cu_a, batch, total_q, G, take, init, local, bs, dt, out
   if (max_pages <= 256)
-    launch_topk_kpl<4, KEY32>(grid, s, P, ps, cu_q, cu_a, batch, total_q, G, take, init, local, bs, out);
+    launch_topk_kpl<4, KEY32>(LS_TOPK_ARGS);
   else if (max_pages <= 1024)
-    launch_topk_kpl<16, KEY32>(grid, s, P, ps, cu_q, cu_a, batch, total_q, G, take, init, local, bs, out);
+    launch_topk_kpl<16, KEY32>(LS_TOPK_ARGS);
   else if (max_pages <= 2048)
-    launch_topk_kpl<32, KEY32>(grid, s, P, ps, cu_q, cu_a, batch, total_q, G, take, init, local, bs, out);
+    launch_topk_kpl<32, KEY32>(LS_TOPK_ARGS);
   else if (max_pages <= 4096)
-    launch_topk_kpl<64, KEY32>(grid, s, P, ps, cu_q, cu_a, batch, total_q, G, take, init, local, bs, out);
+    launch_topk_kpl<64, KEY32>(LS_TOPK_ARGS);
   else if (max_pages <= 8192)
-    launch_topk_kpl<128, KEY32>(grid, s, P, ps, cu_q, cu_a, batch, total_q, G, take, init, local, bs, out);
+    launch_topk_kpl<128, KEY32>(LS_TOPK_ARGS);
+#undef LS_TOPK_ARGS
   else
     return ls_fail(LS_ERR_UNSUPPORTED, "select: at most 8192 pages per sequence (got %d)", max_pages);
   return ls_check_launch("ls_topk_kernel");
@@ -1363,10 +1433,10 @@ static int select_prefill_impl(const char* who, const void* q, int64_t q_row_str
   if (dtype == LS_F32)
     return launch_topk<true>(max_pages, grid, s, ws + L.p, L.p_stride, cu_seqlens_q,
                              cu_seqlens_kc, batch, total_q, G, take, init_blocks, local_blocks,
-                             block_size, topk_idx);
+                             block_size, dtype, topk_idx);
   return launch_topk<false>(max_pages, grid, s, ws + L.p, L.p_stride, cu_seqlens_q,
                             cu_seqlens_kc, batch, total_q, G, take, init_blocks, local_blocks,
-                            block_size, topk_idx);
+                            block_size, dtype, topk_idx);
 }
 
 extern "C" int ls_select_prefill(const void* q, int64_t q_row_stride, int64_t total_q,

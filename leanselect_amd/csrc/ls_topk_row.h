@@ -6,8 +6,21 @@
 
 #include "ls_common.h"
 
-// An emitted page id: -1 above id_max (rows whose kept ids end at a bound).
-__device__ __forceinline__ int32_t ls_topk_id(int id, int id_max) { return id > id_max ? -1 : id; }
+// Order keys whose pages are chosen but emitted as -1: keys above `hi` (NaN
+// scores, whose keys lie above +inf's once NaN is canonical) and the key
+// `ninf` (-inf).  The default rule marks none (no key exceeds 0xffffffff and
+// the empty key 0 is never emitted).
+struct LsInvalidKeys {
+  uint32_t hi = 0xffffffffu;
+  uint32_t ninf = 0u;
+};
+
+// An emitted page id: -1 above id_max (rows whose kept ids end at a bound)
+// and for keys the rule marks invalid.
+__device__ __forceinline__ int32_t ls_topk_id(int id, int id_max, uint32_t key,
+                                              const LsInvalidKeys& rule) {
+  return (id > id_max || key > rule.hi || key == rule.ninf) ? -1 : id;
+}
 
 // ---------------------------------------------------------------------------
 // Top-k page selection.  One wave per row.  The k'-th largest
@@ -23,11 +36,13 @@ __device__ __forceinline__ int32_t ls_topk_id(int id, int id_max) { return id > 
 // kk-th largest key T is found by bisection over the key bits with ballot
 // counts; the winners (key > T, then the first kk - #{key > T} keys equal to
 // T in page order) are written in page order after the lo_end sink pages.
+// Returns T (uniform).
 template <int NS, bool KEY32>
-__device__ __forceinline__ void ls_topk_row(const void* __restrict__ P, int64_t base, int cn,
-                                            int kk, int lo_end, int lane,
-                                            int32_t* __restrict__ orow,
-                                            uint32_t* __restrict__ scr, int id_max) {
+__device__ __forceinline__ uint32_t ls_topk_row(const void* __restrict__ P, int64_t base, int cn,
+                                                int kk, int lo_end, int lane,
+                                                int32_t* __restrict__ orow,
+                                                uint32_t* __restrict__ scr, int id_max,
+                                                const LsInvalidKeys& rule = LsInvalidKeys()) {
   uint32_t key[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
@@ -59,21 +74,24 @@ __device__ __forceinline__ void ls_topk_row(const void* __restrict__ P, int64_t 
     const bool sel = valid && (key[s] > T || (eq && eq_rank < m));
     const uint64_t sel_mask = __ballot(sel);
     const int pos = out_pos + ls_lanes_below(sel_mask);
-    if (sel && pos < lo_end + kk) orow[pos] = ls_topk_id(lo_end + c, id_max);  // exactly kk
+    if (sel && pos < lo_end + kk) orow[pos] = ls_topk_id(lo_end + c, id_max, key[s], rule);  // exactly kk
     out_pos += __popcll(sel_mask);
     eq_before += __popcll(eq_mask);
   }
+  return T;
 }
 
 // The end of ls_topk_row16 for n gathered candidates (key << 16 | column,
 // in column order) held in NP slots of the wave's scratch: the kk-th key T
 // bisected from the common bit prefix of lo and the row maximum m1 (per-lane
 // maxima, reduced here), then the chosen columns written in column order.
+// Returns T (uniform).
 template <int NP>
-__device__ __forceinline__ void ls_topk_emit_packed(const uint32_t* __restrict__ scr, int n,
-                                                    uint32_t lo, uint32_t m1, int kk, int lo_end,
-                                                    int lane, int32_t* __restrict__ orow,
-                                                    int id_max) {
+__device__ __forceinline__ uint32_t ls_topk_emit_packed(const uint32_t* __restrict__ scr, int n,
+                                                        uint32_t lo, uint32_t m1, int kk,
+                                                        int lo_end, int lane,
+                                                        int32_t* __restrict__ orow, int id_max,
+                                                        const LsInvalidKeys& rule = LsInvalidKeys()) {
   uint32_t pk[NP];
 #pragma unroll
   for (int i = 0; i < NP; ++i) pk[i] = i * 64 + lane < n ? scr[i * 64 + lane] : 0u;
@@ -112,10 +130,12 @@ __device__ __forceinline__ void ls_topk_emit_packed(const uint32_t* __restrict__
     const bool sel = valid && (pk[i] > above || (eq && eq_rank < m));
     const uint64_t sel_mask = __ballot(sel);
     const int pos = out_pos + ls_lanes_below(sel_mask);
-    if (sel && pos < lo_end + kk) orow[pos] = ls_topk_id(lo_end + (int)(pk[i] & 0xffffu), id_max);
+    if (sel && pos < lo_end + kk)
+      orow[pos] = ls_topk_id(lo_end + (int)(pk[i] & 0xffffu), id_max, pk[i] >> 16, rule);
     out_pos += __popcll(sel_mask);
     eq_before += __popcll(eq_mask);
   }
+  return T;
 }
 
 // The same for 16-bit scores of rows of more than four slots, emitting from
@@ -127,12 +147,13 @@ __device__ __forceinline__ void ls_topk_emit_packed(const uint32_t* __restrict__
 // from those four slots instead of from all NS.  When more than 256 keys pass
 // (or no bound exists) the row is searched and emitted over all NS slots.
 template <int NS>
-__device__ __forceinline__ void ls_topk_row16(const void* __restrict__ P, int64_t base, int cn,
-                                              int kk, int lo_end, int lane,
-                                              int32_t* __restrict__ orow,
-                                              uint32_t* __restrict__ scr, int id_max) {
+__device__ __forceinline__ uint32_t ls_topk_row16(const void* __restrict__ P, int64_t base, int cn,
+                                                  int kk, int lo_end, int lane,
+                                                  int32_t* __restrict__ orow,
+                                                  uint32_t* __restrict__ scr, int id_max,
+                                                  const LsInvalidKeys& rule = LsInvalidKeys()) {
   if (NS <= 4 || kk < 1 || kk > 128)
-    return ls_topk_row<NS, false>(P, base, cn, kk, lo_end, lane, orow, scr, id_max);
+    return ls_topk_row<NS, false>(P, base, cn, kk, lo_end, lane, orow, scr, id_max, rule);
   // Keys are held shifted up by 16 (order key << 16), so a gathered entry is
   // key | column; 0 marks a column past the row.  Only the slots that reach
   // the row's end (a uniform test) pay for the per-lane column check.
@@ -194,15 +215,15 @@ __device__ __forceinline__ void ls_topk_row16(const void* __restrict__ P, int64_
       const bool sel = valid && (key[s] > T || (eq && eq_rank < m));
       const uint64_t sel_mask = __ballot(sel);
       const int pos = out_pos + ls_lanes_below(sel_mask);
-      if (sel && pos < lo_end + kk) orow[pos] = ls_topk_id(lo_end + c, id_max);
+      if (sel && pos < lo_end + kk) orow[pos] = ls_topk_id(lo_end + c, id_max, key[s], rule);
       out_pos += __popcll(sel_mask);
       eq_before += __popcll(eq_mask);
     }
-    return;
+    return T;
   }
-  if (n <= 64) return ls_topk_emit_packed<1>(scr, n, lo, m1, kk, lo_end, lane, orow, id_max);
-  if (n <= 128) return ls_topk_emit_packed<2>(scr, n, lo, m1, kk, lo_end, lane, orow, id_max);
-  return ls_topk_emit_packed<4>(scr, n, lo, m1, kk, lo_end, lane, orow, id_max);
+  if (n <= 64) return ls_topk_emit_packed<1>(scr, n, lo, m1, kk, lo_end, lane, orow, id_max, rule);
+  if (n <= 128) return ls_topk_emit_packed<2>(scr, n, lo, m1, kk, lo_end, lane, orow, id_max, rule);
+  return ls_topk_emit_packed<4>(scr, n, lo, m1, kk, lo_end, lane, orow, id_max, rule);
 }
 
 
@@ -211,19 +232,25 @@ __device__ __forceinline__ void ls_topk_row16(const void* __restrict__ P, int64_
 // which every lane calls this.  The slot count (uniform) picks one
 // straight-line body, in steps of about an eighth so that a row runs few empty
 // slots; rows of up to four slots are searched over all their keys.
+// Returns the kk-th key T (uniform, the 16-bit order key).
 template <int KPL>
-__device__ __forceinline__ void ls_topk_select16(const void* __restrict__ P, int64_t base, int cn,
-                                                 int kk, int lo_end, int lane,
-                                                 int32_t* __restrict__ orow,
-                                                 uint32_t* __restrict__ scr, int id_max) {
+__device__ __forceinline__ uint32_t ls_topk_select16(const void* __restrict__ P, int64_t base,
+                                                     int cn, int kk, int lo_end, int lane,
+                                                     int32_t* __restrict__ orow,
+                                                     uint32_t* __restrict__ scr, int id_max,
+                                                     const LsInvalidKeys& rule = LsInvalidKeys()) {
   const int n_slots = (cn + 63) >> 6;
-  if (n_slots <= 1) return ls_topk_row<1, false>(P, base, cn, kk, lo_end, lane, orow, scr, id_max);
-  if (n_slots <= 2) return ls_topk_row<2, false>(P, base, cn, kk, lo_end, lane, orow, scr, id_max);
+  if (n_slots <= 1)
+    return ls_topk_row<1, false>(P, base, cn, kk, lo_end, lane, orow, scr, id_max, rule);
+  if (n_slots <= 2)
+    return ls_topk_row<2, false>(P, base, cn, kk, lo_end, lane, orow, scr, id_max, rule);
   if (n_slots <= 4 || KPL <= 4)
-    return ls_topk_row<(KPL < 4 ? KPL : 4), false>(P, base, cn, kk, lo_end, lane, orow, scr, id_max);
+    return ls_topk_row<(KPL < 4 ? KPL : 4), false>(P, base, cn, kk, lo_end, lane, orow, scr,
+                                                   id_max, rule);
 #define LS_TOPK16_CASE(N)                                                                  \
   if (n_slots <= (N) || KPL <= (N))                                                        \
-    return ls_topk_row16<(KPL < (N) ? KPL : (N))>(P, base, cn, kk, lo_end, lane, orow, scr, id_max);
+    return ls_topk_row16<(KPL < (N) ? KPL : (N))>(P, base, cn, kk, lo_end, lane, orow, scr, \
+                                                  id_max, rule);
   LS_TOPK16_CASE(6)
   LS_TOPK16_CASE(8)
   LS_TOPK16_CASE(10)
@@ -240,5 +267,5 @@ __device__ __forceinline__ void ls_topk_select16(const void* __restrict__ P, int
   LS_TOPK16_CASE(64)
   LS_TOPK16_CASE(96)
 #undef LS_TOPK16_CASE
-  return ls_topk_row16<KPL>(P, base, cn, kk, lo_end, lane, orow, scr, id_max);
+  return ls_topk_row16<KPL>(P, base, cn, kk, lo_end, lane, orow, scr, id_max, rule);
 }

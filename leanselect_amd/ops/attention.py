@@ -28,8 +28,15 @@ def sparse_attention(
     block_size: int = 64,
     return_lse: bool = False,
     out: torch.Tensor | None = None,
+    sync_status: bool = False,
 ):
-    """``out [total_q, H, D]`` (and ``lse [H, total_q]`` float32 with ``return_lse``)."""
+    """``out [total_q, H, D]`` (and ``lse [H, total_q]`` float32 with ``return_lse``).
+
+    The kernel reports an expired wait for a staged page in a status word (and
+    writes the affected rows as NaN).  The word is checked without stalling the
+    host: an expired wait raises ``RuntimeError`` at a later attention call or
+    at ``leanselect_amd._hip.attn_status_sync()``; ``sync_status=True`` waits
+    for this call and raises at once."""
     if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
         raise ValueError("q, k, v must be [tokens, heads, head_dim]")
     if topk_idx is None or topk_idx.ndim != 3:
@@ -72,7 +79,8 @@ def sparse_attention(
         topk_idx.data_ptr(), topk_idx.shape[2], block_size, scale, 1 if causal else 0,
         out.data_ptr(), _hip.ptr(lse), ws.data_ptr(), ws.numel(), _hip.stream_of(dev))
     _hip.check(rc, "ls_sparse_attn_varlen")
-    _hip.check_attn_status(ws, "ls_sparse_attn_varlen")
+    if total_q > 0 and batch > 0:  # an empty call launches nothing and leaves no status
+        _hip.check_attn_status(ws, "ls_sparse_attn_varlen", sync=sync_status)
     return (out, lse) if return_lse else out
 
 

@@ -22,7 +22,7 @@ import torch
 from .. import _hip
 
 __all__ = ["n_windows", "kvcache_append", "decode_topk_idx", "sparse_attention_kvcache",
-           "decode_out_len"]
+           "decode_out_len", "stage1_scores"]
 
 
 def n_windows(length: int, kernel_size: int = 32, kernel_stride: int = 16) -> int:
@@ -206,3 +206,45 @@ def sparse_attention_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: to
         _hip.ptr(lse), ws.data_ptr(), ws.numel(), _hip.stream_of(dev))
     _hip.check(rc, "ls_sparse_attn_kvcache")
     return (out, lse) if return_lse else out
+
+
+def stage1_scores(q: torch.Tensor, kc: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                  cu_seqlens_kc: torch.Tensor, max_seqlen_k: int, *,
+                  softmax_scale: float | None = None) -> torch.Tensor:
+    """Decode-form stage-1 scores ``[G, total_q, max_seqlen_k]`` in ``q``'s dtype.
+
+    ``out[g, t, j]`` is the sum over group ``g``'s query heads of
+    ``softmax_j(scale * q[t, h] . kc[cu_seqlens_kc[b] + j, g])`` over the
+    compressed keys of row ``t``'s sequence ``b`` (no causal limit), 0 past
+    them and where the score is NaN (``infllmv2_attn_stage1`` with
+    ``causal=False``, third_party/infllmv2/paper1.patch:2312-2361).  ``q
+    [total_q, H, D]``; ``kc [total_kc, G, D]`` packed by ``cu_seqlens_kc``."""
+    if q.ndim != 3 or kc.ndim != 3:
+        raise ValueError("q must be [total_q, H, D] and kc [total_kc, G, D]")
+    total_q, H, D = q.shape
+    total_kc, G, Dk = kc.shape
+    if Dk != D or H % G or q.dtype != kc.dtype:
+        raise ValueError("q and kc must share head_dim and dtype, H divisible by G")
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("stage-1 scores take bf16 or fp16 inputs")
+    _hip.check_cu_seqlens(cu_seqlens_q, cu_seqlens_kc)
+    dev = _hip.require_gpu(q, kc, cu_seqlens_q, cu_seqlens_kc)
+    B = cu_seqlens_q.numel() - 1
+    cu_host = [int(x) for x in cu_seqlens_kc.tolist()]
+    max_kc = max((cu_host[b + 1] - cu_host[b] for b in range(B)), default=0)
+    out_cols = int(max_seqlen_k)
+    out = torch.zeros((G, total_q, out_cols), dtype=q.dtype, device=dev)
+    if B == 0 or total_q == 0 or out_cols == 0:
+        return out
+    q = q if (q.stride(2) == 1 and q.stride(1) == D) else q.contiguous()
+    kc = kc if (kc.stride(2) == 1 and kc.stride(1) == D) else kc.contiguous()
+    L = _hip.lib()
+    ws = _hip.workspace(L.ls_stage1_scores_workspace_size(total_q, G, max_kc), dev)
+    scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    rc = L.ls_stage1_scores(
+        q.data_ptr(), q.stride(0), cu_seqlens_q.contiguous().data_ptr(), total_q,
+        kc.data_ptr() if total_kc else None, kc.stride(0), cu_seqlens_kc.contiguous().data_ptr(),
+        B, max_kc, H, G, D, _hip.dtype_code(q.dtype), scale, out.data_ptr(), out_cols,
+        ws.data_ptr(), ws.numel(), _hip.stream_of(dev))
+    _hip.check(rc, "ls_stage1_scores")
+    return out

@@ -179,11 +179,13 @@ def nosa_sparse_attention(
     block_size: int = 64,
     return_lse: bool = False,
     out: torch.Tensor | None = None,
+    sync_status: bool = False,
 ):
     """NOSA prefill attention ``out [total_q, H, D]``: for each head, the causal
     keys ``j`` of the row's pages weighted by ``exp(scale * q.k_j + cis[j, g])``
     (``cis [total_k, G]``, finite).  With ``return_lse`` also ``[H, total_q]``
-    float32, the log of the summed weights."""
+    float32, the log of the summed weights.  The status word of the call is
+    checked as ``sparse_attention`` checks it (deferred unless ``sync_status``)."""
     if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
         raise ValueError("q, k, v must be [tokens, heads, head_dim]")
     if topk_idx is None or topk_idx.ndim != 3:
@@ -230,5 +232,6 @@ def nosa_sparse_attention(
         topk_idx.data_ptr(), topk_idx.shape[2], block_size, scale, out.data_ptr(),
         _hip.ptr(lse), ws.data_ptr(), ws.numel(), _hip.stream_of(dev))
     _hip.check(rc, "ls_nosa_attn_varlen")
-    _hip.check_attn_status(ws, "ls_nosa_attn_varlen")
+    if total_q > 0 and batch > 0:  # an empty call launches nothing and leaves no status
+        _hip.check_attn_status(ws, "ls_nosa_attn_varlen", sync=sync_status)
     return (out, lse) if return_lse else out

@@ -23,7 +23,8 @@ import torch
 
 from .selector import LeanSelectSelector
 
-__all__ = ["LayerCase", "head_space_layer", "hidden_space_layer", "planted_pages"]
+__all__ = ["LayerCase", "head_space_layer", "hidden_space_layer", "planted_pages",
+           "UNIT_SCALE"]
 
 
 @dataclass
@@ -45,6 +46,11 @@ class LayerCase:
     @property
     def max_seqlen(self) -> int:
         return max(self.cu_host[i + 1] - self.cu_host[i] for i in range(len(self.cu_host) - 1))
+
+
+# Keyword arguments of ``hidden_space_layer`` for a unit-scale layer: plants
+# that do not accumulate and values of std about 0.5 (hidden 4096).
+UNIT_SCALE = {"accumulate_plants": False, "value_std": 0.4 / 64}
 
 
 def planted_pages(n_blocks: int, init_blocks: int, local_blocks: int, per_block: int,
@@ -138,8 +144,18 @@ def hidden_space_layer(
     weight_std: float = 0.02,
     router_heads: int = 4,
     router_dim: int = 32,
+    accumulate_plants: bool = True,
+    value_std: float | None = None,
 ) -> LayerCase:
-    """MiniCPM4.1-8B attention-layer shape (hidden 4096, 32q/2kv, D 128), packed sequences."""
+    """MiniCPM4.1-8B attention-layer shape (hidden 4096, 32q/2kv, D 128), packed sequences.
+
+    A page planted by several query blocks carries the sum of their topic
+    directions (up to ~56 plants on early pages at 128K, so its keys and values
+    grow with the count).  With ``accumulate_plants=False`` each planted row
+    instead gets ``topic_amp`` times the unit vector of that sum: every row's
+    plant has the same amplitude.  ``value_std`` (default ``weight_std``) is
+    the value projection's std: ``0.4 / sqrt(hidden)`` keeps every value, and so
+    every attention output, well inside (-4, 4)."""
     dev = torch.device(device)
     g = torch.Generator(device=dev).manual_seed(seed)
     gc = torch.Generator(device="cpu").manual_seed(seed + 1)
@@ -153,7 +169,8 @@ def hidden_space_layer(
     wdt = torch.float32
     Wq = torch.randn(hidden, H * D, generator=g, device=dev, dtype=wdt) * weight_std
     Wk = torch.randn(hidden, G * D, generator=g, device=dev, dtype=wdt) * weight_std
-    Wv = torch.randn(hidden, G * D, generator=g, device=dev, dtype=wdt) * weight_std
+    Wv = torch.randn(hidden, G * D, generator=g, device=dev, dtype=wdt) * (
+        weight_std if value_std is None else value_std)
 
     # Topic directions: among random unit candidates keep those whose router
     # alignment q~(u) . k~(u) is largest in the worse of the KV groups.
@@ -192,7 +209,15 @@ def hidden_space_layer(
         planted[b_idx] = plan
         rq, rk = torch.cat(rows_q).to(dev), torch.cat(rows_k).to(dev)
         X.index_add_(0, rq, topic_amp * topics[torch.cat(tq).to(dev)])
-        X.index_add_(0, rk, topic_amp * topics[torch.cat(tk).to(dev)])
+        if accumulate_plants:
+            X.index_add_(0, rk, topic_amp * topics[torch.cat(tk).to(dev)])
+        else:
+            urk, inv = torch.unique(rk, return_inverse=True)
+            acc = torch.zeros(urk.numel(), hidden, device=dev, dtype=wdt)
+            acc.index_add_(0, inv, topics[torch.cat(tk).to(dev)])
+            acc = acc / acc.norm(dim=1, keepdim=True).clamp_min(1e-12)
+            X.index_add_(0, urk, topic_amp * acc)
+            del acc
 
     with torch.no_grad():
         q = (X @ Wq).to(dtype).reshape(N, H, D)

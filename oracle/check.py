@@ -143,19 +143,24 @@ def check_attention(
     *,
     max_abs: float = 2e-2,
     mean_rel: float = 1e-3,
+    literal: bool = False,
 ) -> tuple[bool, float, float]:
     """``(ok, raw max |a - b|, mean relative error)``.
 
     Element bound: ``|a - b| <= max(max_abs, one output-dtype step at |b|)``
     (the step exceeds 2e-2 only for bf16 outputs of magnitude 4 and above);
-    mean bound: ``mean|a - b| / mean|b| <= mean_rel``.
+    with ``literal=True`` the bound is ``max_abs`` alone, with no allowance.
+    Mean bound: ``mean|a - b| / mean|b| <= mean_rel``.
     """
     a = out_test.detach().cpu().to(torch.float64)
     b = out_ref.detach().cpu().to(torch.float64)
     diff = (a - b).abs()
     if not diff.numel():
         return True, 0.0, 0.0
-    tol = output_step(b, out_test.dtype).clamp_min(max_abs)
+    if literal:
+        tol = torch.full_like(b, float(max_abs))
+    else:
+        tol = output_step(b, out_test.dtype).clamp_min(max_abs)
     elem_ok = bool((diff <= tol).all())
     mx = float(diff.max())
     denom = float(b.abs().mean())

@@ -66,7 +66,8 @@ def widest_tile_rows(ids, cu_host, count=2, tile=16):
     return sorted(rows), best
 
 
-def _parity(case, ids, kc, cu_c, rows, *, check_select=True, require_exact=True):
+def _parity(case, ids, kc, cu_c, rows, *, check_select=True, require_exact=True,
+            literal=False):
     if check_select:
         want_ids, scores = oracle_select_rows(case, kc.cpu(), cu_c.cpu().tolist(), rows,
                                               case.q.dtype)
@@ -80,10 +81,53 @@ def _parity(case, ids, kc, cu_c, rows, *, check_select=True, require_exact=True)
     want, _ = oracle.sparse_attention(case.q.cpu(), case.k.cpu(), case.v.cpu(), case.cu_host,
                                       case.cu_host, ids.cpu()[:, rows], rows=rows,
                                       ids_rows_aligned=True)
-    ok, mx, mr = oracle.check_attention(out.cpu()[rows], want)
-    print(f"attention parity: rows={len(rows)} max_abs={mx:.3e} mean_rel={mr:.3e}", flush=True)
+    ok, mx, mr = oracle.check_attention(out.cpu()[rows], want, literal=literal)
+    print(f"attention parity{' (literal 2e-2)' if literal else ''}: rows={len(rows)} "
+          f"max_abs={mx:.3e} mean_rel={mr:.3e} max|out|={want.abs().max().item():.2f}", flush=True)
     assert ok, (mx, mr)
     return out
+
+
+def test_layer_128k_unit_scale_literal_bound():
+    """The headline layer at unit scale: each planted row gets one
+    topic-amplitude vector however many blocks chose its page, and values have
+    std about 0.5, so every output lies inside (-4, 4), where one bf16 step is
+    at most 2^-6.  Selection exact and attention within the literal max-abs
+    2e-2 and mean-relative 1e-3, with no quantisation-step allowance."""
+    case = workloads.hidden_space_layer((131072,), device=DEV, seed=24, **workloads.UNIT_SCALE)
+    kc, cu_c, ids = _select(case)
+    assert not plan_structure_errors(ids, case.cu_host, 64, 1, 4)
+    wide, best = widest_tile_rows(ids, case.cu_host)
+    N = case.cu_host[-1]
+    rows = sorted(set(spread_rows(case.cu_host, per_seq=48)) | set(wide) |
+                  set(range(N - 64, N)))
+    out = _parity(case, ids, kc, cu_c, rows, literal=True)
+    assert float(out.abs().max()) < 4.0
+
+
+def test_c1_layer_fp32_selection_bf16_attention():
+    """The CPU-runnable layer (4096 tokens, 8q/2kv, GQA 4, budget 16 = 1 sink + 2
+    local blocks): selection in float32, bit-exact on every row, and its plans
+    through the bf16 attention kernel (the attention kernels, like the upstream
+    ones, take fp16 and bf16 only) against the oracle on the same bf16 inputs."""
+    case = workloads.head_space_layer(4096, device=DEV)
+    kc, cu_c, ids = _select(case)
+    assert ids.shape == (2, 4096, 16)
+    assert not plan_structure_errors(ids, case.cu_host, 16, 1, 2)
+    rows = list(range(4096))
+    want_ids, scores = oracle_select_rows(case, kc.cpu(), cu_c.cpu().tolist(), rows, torch.float32)
+    rep = oracle.check_topk(ids.cpu(), want_ids, scores, torch.float32)
+    print(f"\nC1 select parity: {rep}", flush=True)
+    assert rep.ok and rep.exact_rows == rep.rows, str(rep)
+    q, k, v = (t.to(torch.bfloat16) for t in (case.q, case.k, case.v))
+    out = sparse_attention(q, k, v, case.cu_seqlens, case.cu_seqlens, 4096, 4096, ids)
+    arows = sorted(set(spread_rows(case.cu_host, per_seq=256)) | set(range(4096 - 64, 4096)))
+    want, _ = oracle.sparse_attention(q.cpu(), k.cpu(), v.cpu(), case.cu_host, case.cu_host,
+                                      ids.cpu()[:, arows], rows=arows, ids_rows_aligned=True)
+    ok, mx, mr = oracle.check_attention(out.cpu()[arows], want, literal=True)
+    print(f"C1 attention parity (bf16, literal 2e-2): rows={len(arows)} max_abs={mx:.3e} "
+          f"mean_rel={mr:.3e}", flush=True)
+    assert ok, (mx, mr)
 
 
 def test_layer_128k_selection_and_attention():

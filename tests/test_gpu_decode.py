@@ -12,7 +12,8 @@ import torch
 
 import oracle
 from leanselect_amd import minicpm
-from leanselect_amd.infllm_v2 import infllmv2_attn_with_kvcache
+from leanselect_amd.infllm_v2 import (infllmv2_attn_stage1, infllmv2_attn_with_kvcache,
+                                      max_pooling_1d_varlen)
 from leanselect_amd.ops import compress_k, decode_topk_idx, kvcache_append, sparse_attention_kvcache
 from leanselect_amd.ops.decode import n_windows
 
@@ -169,6 +170,88 @@ def test_decode_select_all_scores_tied(lens):
     assert torch.equal(ids, want)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_stage1_dropin_scores_match_oracle(dtype):
+    """``infllmv2_attn_stage1(..., causal=False)`` on packed compressed keys
+    against the oracle's stage-1 scores (rounded to the query dtype, 0 past a
+    sequence's keys), including a NaN query row (0 everywhere, as the
+    reference's wrapper maps NaN to 0) and a sequence without keys."""
+    lens = [5000, 700, 20, 2100]  # 20 tokens: no compressed window
+    B, H = len(lens), 32
+    g = torch.Generator().manual_seed(31)
+    nkc = [n_windows(L) for L in lens]
+    cu_kc = _cu(nkc)
+    kc = torch.randn(cu_kc[-1], G, D, generator=g).to(dtype)
+    cu_q = _cu([2, 1, 1, 3])
+    q = torch.randn(cu_q[-1], H, D, generator=g).to(dtype)
+    q[4, 7, 3] = float("nan")
+    max_k = max(nkc) + 5  # wider than every sequence: the tail is 0
+    got = infllmv2_attn_stage1(q.to(DEV), kc.to(DEV), kc.to(DEV), cu_seqlens_q=_i32(cu_q),
+                               cu_seqlens_k=_i32(cu_kc), cu_seqlens_v=_i32(cu_kc),
+                               max_seqlen_q=3, max_seqlen_k=max_k, causal=False)
+    assert got.shape == (G, cu_q[-1], max_k) and got.dtype == dtype
+    raw = oracle.stage1_decode_scores(q, kc, cu_q, cu_kc)
+    want = torch.zeros(G, cu_q[-1], max_k, dtype=torch.float64)
+    want[..., : raw.shape[-1]] = raw
+    want = torch.where(torch.isnan(want), torch.zeros_like(want), want).to(torch.float32).to(dtype)
+    gf, wf = got.cpu().float(), want.float()
+    # Softmax probabilities summed over 16 heads lie in [0, 16]: one rounding
+    # step of the dtype at the value bounds the difference.
+    tol = torch.tensor([oracle.dtype_step(float(x), dtype) for x in wf.flatten()]).view_as(wf)
+    diff = (gf - wf).abs()
+    print(f"\nstage1 drop-in {dtype}: max diff {diff.max().item():.3e}, "
+          f"exact {(diff == 0).float().mean().item():.4f}")
+    assert bool((diff <= tol + 1e-7).all())
+    assert bool((got[0, 4].cpu() == 0).all())  # the NaN row (group 0 holds head 7)
+    assert not bool(got.isnan().any())
+    seq_of = [b for b in range(B) for _ in range(cu_q[b + 1] - cu_q[b])]
+    for t, b in enumerate(seq_of):  # past the sequence's keys: exactly 0
+        assert bool((got[:, t, nkc[b]:].cpu() == 0).all())
+    with pytest.raises(NotImplementedError):
+        infllmv2_attn_stage1(q.to(DEV), kc.to(DEV), kc.to(DEV), cu_seqlens_q=_i32(cu_q),
+                             cu_seqlens_k=_i32(cu_kc), cu_seqlens_v=_i32(cu_kc),
+                             max_seqlen_q=3, max_seqlen_k=max_k, causal=True)
+
+
+def test_reference_decode_selection_from_the_dropins():
+    """The reference's decode selection (compressed_attention with cache_lens,
+    leanselect/models/minicpm.py:617-705) composed from the drop-ins alone --
+    stage-1 scores, bf16, max_pooling_1d_varlen, top-k, sort, ids past the
+    row's page to -1 -- gives ``decode_topk_idx``'s plans (gap-aware: the
+    composition's torch.topk breaks ties its own way)."""
+    lens = [40000, 9000, 3000]
+    cap = max(lens)
+    k, v, kc_cache, _, _ = _filled_cache(lens, cap, seed=33)
+    del k, v
+    B, H, bs, topk, local, init = len(lens), 32, 64, 64, 4, 1
+    g = torch.Generator().manual_seed(34)
+    q = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    cu_q = list(range(B + 1))
+    nkc = [n_windows(L) for L in lens]
+    cu_kc = _cu(nkc)
+    kc = torch.cat([kc_cache[b, :nkc[b]] for b in range(B)])
+    cache_lens = [L - 1 for L in lens]  # the reference's cache_lens = seq_lens_k - 1
+    score = infllmv2_attn_stage1(q, kc, kc, cu_seqlens_q=_i32(cu_q), cu_seqlens_k=_i32(cu_kc),
+                                 cu_seqlens_v=_i32(cu_kc), max_seqlen_q=1,
+                                 max_seqlen_k=max(nkc), causal=False)
+    score = score.to(torch.bfloat16)
+    block = max_pooling_1d_varlen(score.contiguous(), _i32(cu_q), _i32(cu_kc), _i32(cache_lens),
+                                  1, max(nkc), local_blocks=local, init_blocks=init,
+                                  block_size=bs, stride=16)
+    kk = min(topk, block.shape[-1])
+    comp = block.topk(kk, dim=-1).indices.sort(-1).values
+    q_idx = torch.tensor([c // bs for c in cache_lens], device=DEV)
+    comp[comp > q_idx[None, :, None]] = -1
+    comp = comp.to(torch.int32)
+    ids = decode_topk_idx(q, kc_cache, _i32(lens), _i32(cu_q), topk=topk, local_blocks=local,
+                          init_blocks=init)
+    assert comp.shape == ids.shape
+    rep = oracle.check_topk(comp.cpu(), ids.cpu(), block.cpu().double(), torch.bfloat16,
+                            ulp_band=1.0)
+    print(f"\nreference decode selection from the drop-ins: {rep}")
+    assert rep.ok, str(rep)
+
+
 def _packed(k, v, lens):
     return (torch.cat([k[b, :L].cpu() for b, L in enumerate(lens)]),
             torch.cat([v[b, :L].cpu() for b, L in enumerate(lens)]))
@@ -252,6 +335,28 @@ def test_with_kvcache_dropin_appends_and_attends():
                                    _cu(new_lens), all_ids, causal=False)[0]
     ok, mx, mr = oracle.check_attention(dense.view(B, H, D).cpu(), want)
     assert ok, (mx, mr)
+
+
+def test_with_kvcache_dense_beyond_256_pages():
+    """``topk_idx=None`` over caches of more than 256 pages (16384 tokens): the
+    pages are attended in groups merged by their log-sum-exp, against the oracle
+    over every page; a short sequence beside a long one has groups with no key."""
+    B, cap, H = 2, 20480, 16
+    lens = [20000, 5000]
+    k, v, _, kp, vp = _filled_cache(lens, cap, seed=21)
+    g = torch.Generator().manual_seed(22)
+    q = torch.randn(B, 1, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    out, lse = infllmv2_attn_with_kvcache(q, k, v, cache_seqlens=_i32(lens),
+                                          return_softmax_lse=True)
+    n_pages = -(-max(lens) // 64)
+    all_ids = torch.arange(n_pages, dtype=torch.int32).expand(G, B, n_pages).contiguous()
+    want, want_lse = oracle.sparse_attention(q.view(B, H, D).cpu(), kp, vp, list(range(B + 1)),
+                                             _cu(lens), all_ids, causal=False)
+    ok, mx, mr = oracle.check_attention(out.view(B, H, D).cpu(), want)
+    print(f"\ndense kvcache {lens}: max_abs={mx:.3e} mean_rel={mr:.3e}")
+    assert ok, (mx, mr)
+    got_lse = lse.permute(1, 0, 2).reshape(H, B).cpu().double()
+    torch.testing.assert_close(got_lse, want_lse.double(), rtol=0, atol=2e-3)
 
 
 def test_model_decode_matches_prefill_when_every_page_is_kept():

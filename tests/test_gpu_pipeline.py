@@ -9,6 +9,7 @@ from gpu_helpers import oracle_select_rows, plan_structure_errors, spread_rows
 from leanselect_amd import _hip, workloads
 from leanselect_amd.ops import compress_k, leanselect_prefill_topk_idx, sparse_attention
 from leanselect_amd.ops.attention import infllmv2_attn_varlen_func
+from leanselect_amd.ops.nosa import nosa_sparse_attention
 from leanselect_amd.prefill import leanselect_sparse_prefill
 
 pytestmark = pytest.mark.gpu
@@ -238,19 +239,27 @@ def test_end_to_end_prefill_32k_sampled():
 
 def test_ring_wait_expiry_is_reported():
     """With the wait bound forced to zero from the host every ring wait expires at
-    once: the kernel still finishes, the status word is set and the wrapper raises,
-    and the rows of the waves whose wait expired are NaN.  The next call with the
-    default bound is clean and correct."""
+    once: the kernel still finishes, the status word is set and the wrapper raises
+    (at once with ``sync_status``; at ``attn_status_sync`` otherwise, without the
+    call itself waiting), and the rows of the waves whose wait expired are NaN.
+    The next call with the default bound is clean and correct."""
     case, ids = _attention_case(lens=(3000,), seed=4)
     L = _hip.lib()
     out = torch.zeros_like(case.q)
+    _hip.attn_status_sync()  # nothing earlier is pending
     L.ls_attn_set_spin_limit(0)
     try:
         with pytest.raises(RuntimeError, match="expired"):
             sparse_attention(case.q, case.k, case.v, case.cu_seqlens, case.cu_seqlens,
-                             3000, 3000, ids, out=out)
+                             3000, 3000, ids, out=out, sync_status=True)
+        out2 = torch.zeros_like(case.q)
+        sparse_attention(case.q, case.k, case.v, case.cu_seqlens, case.cu_seqlens,
+                         3000, 3000, ids, out=out2)  # deferred: returns without raising
+        with pytest.raises(RuntimeError, match="expired"):
+            _hip.attn_status_sync()
     finally:
         L.ls_attn_set_spin_limit(-1)
+    _hip.attn_status_sync()  # the queue is drained
     nan_rows = torch.isnan(out.float()).any(dim=2).any(dim=1)
     assert bool(nan_rows.any())
     # a row is either NaN in every head of a group or has finite values there
@@ -258,6 +267,31 @@ def test_ring_wait_expiry_is_reported():
     assert bool((per_group.all(dim=2) == per_group.any(dim=2)).all())
     rows = spread_rows(case.cu_host, per_seq=32)
     _check_attention(case, ids, rows)
+    _hip.attn_status_sync()
+
+
+def test_empty_attention_calls_read_no_stale_status():
+    """Calls with no query rows (or no sequences) launch no kernel, so they must
+    not read a status word: the workspace then holds whatever the allocator's
+    reused block held.  A freed block of 0xFF bytes comes first."""
+    junk = torch.full((1 << 20,), 255, dtype=torch.uint8, device=DEV)
+    del junk
+    G, H, D = 2, 8, 128
+    q = torch.empty(0, H, D, dtype=torch.bfloat16, device=DEV)
+    k = torch.randn(128, G, D, device=DEV).to(torch.bfloat16)
+    v = torch.randn(128, G, D, device=DEV).to(torch.bfloat16)
+    ids = torch.empty(G, 0, 4, dtype=torch.int32, device=DEV)
+    cu_q = torch.zeros(2, dtype=torch.int32, device=DEV)
+    cu_k = torch.tensor([0, 128], dtype=torch.int32, device=DEV)
+    out = sparse_attention(q, k, v, cu_q, cu_k, 0, 128, ids, sync_status=True)
+    assert out.shape == (0, H, D)
+    out = nosa_sparse_attention(q, k, v, torch.zeros(128, G, device=DEV), cu_q, cu_k, 0, 128,
+                                ids, sync_status=True)
+    assert out.shape == (0, H, D)
+    none = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = sparse_attention(q, k, v, none, none, 0, 0, ids, sync_status=True)
+    assert out.shape == (0, H, D)
+    _hip.attn_status_sync()
 
 
 def test_prefill_step_graph_replays_match_eager():

@@ -53,6 +53,28 @@ def test_noalloc_matches_the_workspace_entry_point():
         assert torch.equal(lse, want_lse)
 
 
+@pytest.mark.gpu
+def test_noalloc_empty_call_writes_a_clean_status():
+    """A call with no query rows launches no attention kernel; the caller's
+    status word (pre-filled with -1 here) is still written with 0."""
+    L = _hip.lib()
+    G, H, D = 2, 8, 128
+    q = torch.empty(0, H, D, dtype=torch.bfloat16, device="cuda")
+    k = torch.randn(128, G, D, device="cuda").to(torch.bfloat16)
+    cu_q = torch.zeros(2, dtype=torch.int32, device="cuda")
+    cu_k = torch.tensor([0, 128], dtype=torch.int32, device="cuda")
+    ids = torch.empty(G, 0, 4, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    rc = L.ls_sparse_attn_varlen_noalloc(
+        q.data_ptr(), H * D, k.data_ptr(), G * D, k.data_ptr(), G * D, cu_q.data_ptr(),
+        cu_k.data_ptr(), 1, 0, 128, 0, 128, H, G, D, _hip.LS_BF16, ids.data_ptr(), 4, 64, -1.0,
+        1, out.data_ptr(), None, status.data_ptr(), _hip.stream_of(q.device))
+    _hip.check(rc, "ls_sparse_attn_varlen_noalloc")
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+
+
 def test_noalloc_rejects_requests_above_the_static_scratch():
     # 2 KV heads x 1100 pages of staged K/V exceed 64 MiB; nothing is dereferenced
     # and no device is touched before the size check.
