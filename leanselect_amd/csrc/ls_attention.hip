@@ -111,6 +111,9 @@ __global__ void ls_attn_status_clear_kernel(int32_t* __restrict__ status) {
 #ifndef LS_ATT_XCD_CHUNK
 #define LS_ATT_XCD_CHUNK 32                  // consecutive tiles per XCD run
 #endif
+#ifndef LS_ATT_SHARE_STRIDED
+#define LS_ATT_SHARE_STRIDED 25              // plan ids per union page (x10) for the strided order
+#endif
 #ifndef LS_ATT_SPIN_SLEEP
 #define LS_ATT_SPIN_SLEEP 1                  // s_sleep units between a waiting wave's polls
 #endif
@@ -359,14 +362,19 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   for (int i = 0; i < LS_ATT_WAVES; ++i) n_union += s_wsum[i];
   const int32_t* vexp_seq = vexp + (int64_t)g * n_pages_ws + pg_off[b];
   const float inv_scale_log2 = 1.f / scale_log2;
-  // The pages are visited in a strided order (ascending page i goes to slot
-  // i * stride mod n_union, a bijection for stride coprime to n_union):
-  // neighbouring pages tend to be selected by the same rows, and spreading
-  // them out evens the work of the waves over any window of pages.
-  // (Empty or one-page lists keep stride 1; a coprime odd stride below 64 + 7
-  // exists for any list this kernel accepts, the loop bound only caps it.)
+  // Page order.  Where the rows share many pages (at least
+  // LS_ATT_SHARE_STRIDED / 10 plan ids per union page) the pages are visited in
+  // a strided order (ascending page i goes to slot i * stride mod n_union, a
+  // bijection for stride coprime to n_union): neighbouring pages tend to be
+  // selected by the same rows, and spreading them out evens the work of the
+  // waves over any window of pages.  Where they share few, ascending order:
+  // the tiles running side by side on an XCD then reach a shared page at
+  // nearly the same time, while it is still in that XCD's L2, and the waves'
+  // work is even anyway.  (Empty or one-page lists keep stride 1; a coprime
+  // odd stride below 64 + 7 exists for any list this kernel accepts, the loop
+  // bound only caps it.)
   int stride = 1;
-  if (n_union > 1) {
+  if (n_union > 1 && 10 * n_rows * take >= LS_ATT_SHARE_STRIDED * n_union) {
     for (int cand = 7; cand < 71; cand += 2) {
       int a = cand, b = n_union;
       while (b) {
