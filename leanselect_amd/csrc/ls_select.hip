@@ -716,6 +716,36 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_panel_kernel(
     for (int ks = 0; ks < KS; ++ks)
       kf[ks] = *reinterpret_cast<const ls_u32x4*>(kb + r * ROWB + 16 * ((4 * ks + q) ^ r));
   };
+  auto step_mfma = [&](const ls_u32x4 (&kf)[KS], ls_f32x4 (&acc)[4]) {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      acc[tb] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) acc[tb] = LsElem<DT>::mfma(kf[ks], qf[tb][ks], acc[tb]);
+    }
+  };
+  // The page maxima of step j from its scores acc (atoms past the end are
+  // masked when `tail`), staged in LDS.
+  auto step_epi = [&](int j, ls_f32x4 (&acc)[4], bool tail) {
+    const int atom0 = 16 * j + 4 * q;
+    if (tail) {
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (atom0 + i >= n_at) acc[tb][i] = -INFINITY;
+    }
+    float rot[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) rot[tb] = ls_shfl(acc[tb][3], (lane - 16) & 63);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const float m4 = ls_fmax_nan(ls_fmax_nan(acc[tb][0], acc[tb][1]), ls_fmax_nan(acc[tb][2], acc[tb][3]));
+      const float prev = q == 0 ? carry[tb] : rot[tb];
+      carry[tb] = rot[tb];
+      so[(16 * tb + r) * SP + 4 * (j & 15) + q] = LsElem<DT>::from_f(ls_canon_nan(ls_fmax_nan(m4, prev)));
+    }
+  };
   auto step = [&](int j, const ls_u32x4 (&kf)[KS]) {
     ls_f32x4 acc[4];
 #pragma unroll
@@ -761,11 +791,26 @@ __global__ __launch_bounds__(256, KS <= 4 ? 3 : 2) void ls_score_panel_kernel(
     // computes (two fragment sets used in turn).
     ls_u32x4 kf[2][KS];
     read_k(kf[0], &s_k[buf][0]);
+    if (jb >= j_first && jb + NSTEP - 1 <= jw_hi && 16 * (jb + NSTEP) <= n_at) {
+      // Every step of the batch is the wave's and has all its atoms: branch
+      // free, with step st + 1's MFMAs issued before step st's maxima, so the
+      // vector work overlaps the matrix core.
+      ls_f32x4 acc[2][4];
+      step_mfma(kf[0], acc[0]);
+      read_k(kf[1], &s_k[buf][STEPB]);
 #pragma unroll
-    for (int st = 0; st < NSTEP; ++st) {
-      const int j = jb + st;
-      if (st + 1 < NSTEP) read_k(kf[(st + 1) & 1], &s_k[buf][(st + 1) * STEPB]);
-      if (j >= j_first && j <= jw_hi) step(j, kf[st & 1]);
+      for (int st = 0; st < NSTEP; ++st) {
+        if (st + 1 < NSTEP) step_mfma(kf[(st + 1) & 1], acc[(st + 1) & 1]);
+        if (st + 2 < NSTEP) read_k(kf[st & 1], &s_k[buf][(st + 2) * STEPB]);
+        step_epi(jb + st, acc[st & 1], false);
+      }
+    } else {
+#pragma unroll
+      for (int st = 0; st < NSTEP; ++st) {
+        const int j = jb + st;
+        if (st + 1 < NSTEP) read_k(kf[(st + 1) & 1], &s_k[buf][(st + 1) * STEPB]);
+        if (j >= j_first && j <= jw_hi) step(j, kf[st & 1]);
+      }
     }
     // The wave's last step, or a block's last step, was in this batch.
     const int jl = min(jb + NSTEP - 1, jw_hi);
