@@ -27,6 +27,18 @@ enum { LS_F32 = 0, LS_BF16 = 1, LS_F16 = 2 };
 
 enum { LS_ATTN_RING_TIMEOUT = 1 };
 
+/*
+ * Column range of the varlen page max-pool (argument `clip`): a row of
+ * sequence b pools the columns [0, cu_seqlens_k[b + 1] - cu_seqlens_k[b]) of
+ * its score row (LS_POOL_CLIP_SEQUENCE) or the whole padded row [0,
+ * max_seqlen_k) (LS_POOL_CLIP_ROW).  The two differ only where a shorter
+ * sequence's padding columns hold values above -inf (the CIS window means
+ * are 0 there).  The upstream kernel body that fixes this choice is not part
+ * of the reference tree (third_party/infllmv2/paper1.patch:1831-1860 shows
+ * only its offsets).
+ */
+enum { LS_POOL_CLIP_SEQUENCE = 0, LS_POOL_CLIP_ROW = 1 };
+
 enum {
   LS_OK = 0,
   LS_ERR_INVALID = 1,     /* bad shape, geometry or pointer */
@@ -304,8 +316,9 @@ int ls_cis_mean_pool(const void* cis, int64_t cis_row_stride, int64_t total_n,
  * Row t of sequence b has page off = (t - cu_seqlens_q[b] + cache_lens[b]) /
  * block_size.  Page p is +inf when p < init_blocks or off - local_blocks <= p
  * <= off, else the max of input[h, t, j] over j in [p s - 1, p s + s) clipped
- * to [0, min(cu_seqlens_k[b + 1] - cu_seqlens_k[b], max_seqlen_k)) (-inf when
- * empty), s = block_size / stride.
+ * to [0, min(cu_seqlens_k[b + 1] - cu_seqlens_k[b], max_seqlen_k))
+ * (clip = LS_POOL_CLIP_SEQUENCE) or to [0, max_seqlen_k) (LS_POOL_CLIP_ROW),
+ * -inf when empty, s = block_size / stride.
  * Replaces infllm_v2.max_pooling_1d_varlen (third_party/infllmv2/paper1.patch:2664-2760,
  * called at leanselect/models/nosa.py:1263-1286).
  */
@@ -313,8 +326,8 @@ int ls_page_maxpool_varlen(const void* input, const int32_t* cu_seqlens_q,
                            const int32_t* cu_seqlens_k, const int32_t* cache_lens, int32_t batch,
                            int32_t num_heads, int64_t total_q, int64_t max_seqlen_k,
                            int64_t out_len, int32_t local_blocks, int32_t init_blocks,
-                           int32_t block_size, int32_t stride, int32_t dtype, void* out,
-                           void* stream);
+                           int32_t block_size, int32_t stride, int32_t clip, int32_t dtype,
+                           void* out, void* stream);
 
 /*
  * Workspace bytes needed by ls_nosa_select_prefill (max_pages =
@@ -328,13 +341,17 @@ size_t ls_nosa_select_workspace_size(int64_t total_q, int64_t total_atoms, int32
 /*
  * NOSA prefill page plans, the LeanSelect branch of compressed_attention:
  *   1. qk page scores: the folded-router atom scores (as ls_select_prefill),
- *      max-pooled to pages with sink and local pages +inf, no causal mask;
+ *      max-pooled to pages with sink and local pages +inf, no causal mask
+ *      (-inf past the sequence's atoms, so the clip does not change them);
  *   2. the min(init + local + select, out_len) best qk pages (ties to the
  *      lower page) form a shortlist;
  *   3. CIS page scores: CIS window means (cis [total_k, num_kv_heads], rows
  *      cis_row_stride apart, of cis_dtype; windows of sequence b per
- *      cu_seqlens_k) max-pooled to pages, sink/local pages +inf, pages after
- *      q_idx -inf, shortlisted pages +inf;
+ *      cu_seqlens_k; 0 past the sequence's windows up to the longest
+ *      sequence's count) max-pooled to pages under `pool_clip` (an
+ *      LS_POOL_CLIP_* value: the sequence's own windows, or every column up
+ *      to the longest sequence's window count), sink/local pages +inf, pages
+ *      after q_idx -inf, shortlisted pages +inf;
  *   4. topk_idx [num_kv_heads, total_q, take] int32: the take = min(topk,
  *      out_len) best pages, ascending, ids after q_idx replaced by -1.
  * out_len = ceil(max_seqlen_q / block_size); q_idx = (t - cu_seqlens_q[b] +
@@ -352,8 +369,8 @@ int ls_nosa_select_prefill(const void* q, int64_t q_row_stride, int64_t total_q,
                            const float* k_proj, int32_t router_heads, int32_t router_dim,
                            int32_t dtype, int32_t topk, int32_t block_size,
                            int32_t kernel_stride, int32_t init_blocks, int32_t local_blocks,
-                           int32_t select_blocks, int32_t* topk_idx, int32_t take,
-                           void* workspace, size_t workspace_bytes, void* stream);
+                           int32_t select_blocks, int32_t pool_clip, int32_t* topk_idx,
+                           int32_t take, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Workspace bytes needed by ls_nosa_attn_varlen.

@@ -16,6 +16,15 @@ LIB_PATH = Path(__file__).resolve().with_name("libleanselect_hip.so")
 LS_F32, LS_BF16, LS_F16 = 0, 1, 2
 LS_OK, LS_ERR_INVALID, LS_ERR_UNSUPPORTED, LS_ERR_WORKSPACE, LS_ERR_HIP = range(5)
 LS_ATTN_RING_TIMEOUT = 1
+LS_POOL_CLIP_SEQUENCE, LS_POOL_CLIP_ROW = 0, 1
+POOL_CLIPS = {"sequence": LS_POOL_CLIP_SEQUENCE, "row": LS_POOL_CLIP_ROW}
+
+
+def pool_clip_code(clip: str) -> int:
+    try:
+        return POOL_CLIPS[clip]
+    except KeyError:
+        raise ValueError(f"unknown pool clip {clip!r}; expected 'sequence' or 'row'") from None
 
 _i32, _i64, _f32, _sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 _p = ctypes.c_void_p
@@ -59,14 +68,14 @@ SIGNATURES = {
     "ls_cis_mean_pool": (
         _i32, [_p, _i64, _i64, _i32, _p, _i32, _i32, _i32, _i32, _i32, _p, _i32, _p]),
     "ls_page_maxpool_varlen": (
-        _i32, [_p, _p, _p, _p, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p,
-               _p]),
+        _i32, [_p, _p, _p, _p, _i32, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32,
+               _p, _p]),
     "ls_nosa_select_workspace_size": (
         _sz, [_i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "ls_nosa_select_prefill": (
         _i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _p, _i32, _i32, _i32,
                _i32, _i32, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-               _p, _i32, _p, _sz, _p]),
+               _i32, _p, _i32, _p, _sz, _p]),
     "ls_nosa_attn_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32]),
     "ls_nosa_attn_varlen": (
         _i32, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32, _p, _p, _i32, _i64, _i64, _i32,

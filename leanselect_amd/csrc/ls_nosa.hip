@@ -80,20 +80,22 @@ extern "C" int ls_cis_mean_pool(const void* cis, int64_t cis_row_stride, int64_t
 // in [Hk][total_q][max_k] -> out [Hk][total_q][out_len].  Row t of sequence b
 // has page off_bq = (t - cu_q[b] + cache_len[b]) / block_size; page p is +inf
 // when p < init_blocks or off_bq - local_blocks <= p <= off_bq, else the max of
-// in[h][t][j] over j in [p*s - 1, p*s + s) clipped to the sequence's
-// cu_k[b + 1] - cu_k[b] columns (-inf when empty), s = block_size / stride.
-// One workgroup per (row, head), threads over pages (the reference's grid).
+// in[h][t][j] over j in [p*s - 1, p*s + s) clipped to [0, lk) (-inf when
+// empty), s = block_size / stride.  lk is the sequence's cu_k[b + 1] - cu_k[b]
+// columns (LS_POOL_CLIP_SEQUENCE, at most max_k) or the row width max_k
+// (LS_POOL_CLIP_ROW).  One workgroup per (row, head), threads over pages (the
+// reference's grid).
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(256) void ls_page_maxpool_kernel(
     const typename LsElem<DT>::T* __restrict__ in, const int32_t* __restrict__ cu_q,
     const int32_t* __restrict__ cu_k, const int32_t* __restrict__ cache_lens, int batch,
     int64_t total_q, int64_t max_k, int64_t out_len, int s, int block_size, int init_blocks,
-    int local_blocks, typename LsElem<DT>::T* __restrict__ out) {
+    int local_blocks, int clip_row, typename LsElem<DT>::T* __restrict__ out) {
   const int64_t t = blockIdx.x;
   const int h = blockIdx.y;
   const int b = ls_find_segment(cu_q, batch, t);
-  const int64_t lk = min((int64_t)(cu_k[b + 1] - cu_k[b]), max_k);
+  const int64_t lk = clip_row ? max_k : min((int64_t)(cu_k[b + 1] - cu_k[b]), max_k);
   const int64_t off_bq = (t - cu_q[b] + cache_lens[b]) / block_size;
   const typename LsElem<DT>::T* row = in + ((int64_t)h * total_q + t) * max_k;
   typename LsElem<DT>::T* orow = out + ((int64_t)h * total_q + t) * out_len;
@@ -116,13 +118,15 @@ extern "C" int ls_page_maxpool_varlen(const void* input, const int32_t* cu_seqle
                                       int32_t batch, int32_t num_heads, int64_t total_q,
                                       int64_t max_seqlen_k, int64_t out_len, int32_t local_blocks,
                                       int32_t init_blocks, int32_t block_size, int32_t stride,
-                                      int32_t dtype, void* out, void* stream) {
+                                      int32_t clip, int32_t dtype, void* out, void* stream) {
   LS_REQUIRE(batch >= 0 && num_heads >= 0 && total_q >= 0 && max_seqlen_k >= 0 && out_len >= 0,
              LS_ERR_INVALID, "ls_page_maxpool_varlen: bad sizes");
   LS_REQUIRE(block_size > 0 && stride > 0 && block_size % stride == 0, LS_ERR_INVALID,
              "ls_page_maxpool_varlen: block_size must be a positive multiple of stride");
   LS_REQUIRE(dtype == LS_F32 || dtype == LS_BF16 || dtype == LS_F16, LS_ERR_INVALID,
              "ls_page_maxpool_varlen: unknown dtype %d", dtype);
+  LS_REQUIRE(clip == LS_POOL_CLIP_SEQUENCE || clip == LS_POOL_CLIP_ROW, LS_ERR_INVALID,
+             "ls_page_maxpool_varlen: unknown clip %d", clip);
   LS_REQUIRE(total_q <= 0x7fffffffLL && num_heads <= 65535, LS_ERR_UNSUPPORTED,
              "ls_page_maxpool_varlen: too many rows or heads");
   if (total_q == 0 || num_heads == 0 || out_len == 0 || batch == 0) return LS_OK;
@@ -134,55 +138,61 @@ extern "C" int ls_page_maxpool_varlen(const void* input, const int32_t* cu_seqle
   if (dtype == LS_BF16)
     hipLaunchKernelGGL(ls_page_maxpool_kernel<LS_BF16>, grid, dim3(256), 0, s, (const uint16_t*)input,
                        cu_seqlens_q, cu_seqlens_k, cache_lens, batch, total_q, max_seqlen_k,
-                       out_len, sp, block_size, init_blocks, local_blocks, (uint16_t*)out);
+                       out_len, sp, block_size, init_blocks, local_blocks, clip, (uint16_t*)out);
   else if (dtype == LS_F16)
     hipLaunchKernelGGL(ls_page_maxpool_kernel<LS_F16>, grid, dim3(256), 0, s, (const uint16_t*)input,
                        cu_seqlens_q, cu_seqlens_k, cache_lens, batch, total_q, max_seqlen_k,
-                       out_len, sp, block_size, init_blocks, local_blocks, (uint16_t*)out);
+                       out_len, sp, block_size, init_blocks, local_blocks, clip, (uint16_t*)out);
   else
     hipLaunchKernelGGL(ls_page_maxpool_kernel<LS_F32>, grid, dim3(256), 0, s, (const float*)input,
                        cu_seqlens_q, cu_seqlens_k, cache_lens, batch, total_q, max_seqlen_k,
-                       out_len, sp, block_size, init_blocks, local_blocks, (float*)out);
+                       out_len, sp, block_size, init_blocks, local_blocks, clip, (float*)out);
   return ls_check_launch("ls_page_maxpool_kernel");
 }
 
 // ---------------------------------------------------------------------------
 // Fused-path CIS page scores: cpg[g][pg_off[b] + p] = max over the CIS window
-// means m in [4p - 1, 4p + 4) ∩ [0, A_b) of sequence b (each mean rounded to
-// the CIS dtype, as the drop-in pooling stores it; 0 for a window that does
-// not fit in the sequence's keys), for p <= A_b / 4.
-// pg_off[b] = sum over earlier sequences of (A_b > 0 ? A_b / 4 + 1 : 0).
+// means m in [4p - 1, 4p + 4) ∩ [0, W) of sequence b, for p <= A_b / 4 (each
+// mean rounded to the CIS dtype, as the drop-in pooling stores it; 0 for a
+// window that does not fit in the sequence's keys and for m >= A_b).  W = A_b
+// under LS_POOL_CLIP_SEQUENCE, W = A_max = max_b A_b (the width of the
+// window-mean rows) under LS_POOL_CLIP_ROW.
+// pg_off[b] = sum over earlier sequences of (A_b > 0 ? A_b / 4 + 1 : 0);
+// pg_off[batch + 1] = A_max.
 // ---------------------------------------------------------------------------
 __global__ void ls_nosa_plan_kernel(const int32_t* __restrict__ cu_a, int batch,
                                     int32_t* __restrict__ pg_off) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int32_t acc = 0;
+  int32_t acc = 0, a_max = 0;
   pg_off[0] = 0;
   for (int b = 0; b < batch; ++b) {
     const int a = cu_a[b + 1] - cu_a[b];
     acc += a > 0 ? a / 4 + 1 : 0;
+    a_max = a > a_max ? a : a_max;
     pg_off[b + 1] = acc;
   }
+  pg_off[batch + 1] = a_max;
 }
 
 template <int CT>
 __global__ __launch_bounds__(256) void ls_nosa_cis_pages_kernel(
     const typename LsElem<CT>::T* __restrict__ cis, int64_t cis_rs, const int32_t* __restrict__ cu_k,
     const int32_t* __restrict__ cu_a, const int32_t* __restrict__ pg_off, int batch,
-    int64_t n_pages_launch, float* __restrict__ cpg, int64_t cpg_g_stride) {
+    int clip_row, int64_t n_pages_launch, float* __restrict__ cpg, int64_t cpg_g_stride) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int g = blockIdx.y;
   if (i >= pg_off[batch] || i >= n_pages_launch) return;
   const int b = ls_find_segment(pg_off, batch, i);
   const int p = (int)(i - pg_off[b]);
   const int A = cu_a[b + 1] - cu_a[b];
+  const int W = clip_row ? pg_off[batch + 1] : A;
   const int64_t start = cu_k[b], n_k = (int64_t)cu_k[b + 1] - start;
   float best = -INFINITY;
   const int lo = 4 * p - 1 < 0 ? 0 : 4 * p - 1;
-  const int hi = 4 * p + 4 < A ? 4 * p + 4 : A;
+  const int hi = 4 * p + 4 < W ? 4 * p + 4 : W;
   for (int m = lo; m < hi; ++m) {
     float acc = 0.f;
-    if ((int64_t)m * 16 + 32 <= n_k)  // a window past the sequence end pools to 0
+    if (m < A && (int64_t)m * 16 + 32 <= n_k)  // a window past the sequence end pools to 0
       for (int j = 0; j < 32; ++j)
         acc += LsElem<CT>::to_f(cis[(start + (int64_t)m * 16 + j) * cis_rs + g]);
     best = fmaxf(best, LsElem<CT>::to_f(LsElem<CT>::from_f(acc * (1.f / 32.f))));
@@ -192,7 +202,8 @@ __global__ __launch_bounds__(256) void ls_nosa_cis_pages_kernel(
 
 int ls_nosa_cis_pages_launch(const void* cis, int64_t cis_rs, int cis_dtype, const int32_t* cu_k,
                              const int32_t* cu_a, int batch, int64_t total_atoms, int G,
-                             int32_t* pg_off, float* cpg, int64_t cpg_g_stride, hipStream_t s) {
+                             int clip_row, int32_t* pg_off, float* cpg, int64_t cpg_g_stride,
+                             hipStream_t s) {
   hipLaunchKernelGGL(ls_nosa_plan_kernel, dim3(1), dim3(64), 0, s, cu_a, batch, pg_off);
   int rc = ls_check_launch("ls_nosa_plan_kernel");
   if (rc) return rc;
@@ -201,13 +212,16 @@ int ls_nosa_cis_pages_launch(const void* cis, int64_t cis_rs, int cis_dtype, con
   const dim3 grid((unsigned)((n + 255) / 256), G);
   if (cis_dtype == LS_BF16)
     hipLaunchKernelGGL(ls_nosa_cis_pages_kernel<LS_BF16>, grid, dim3(256), 0, s,
-                       (const uint16_t*)cis, cis_rs, cu_k, cu_a, pg_off, batch, n, cpg, cpg_g_stride);
+                       (const uint16_t*)cis, cis_rs, cu_k, cu_a, pg_off, batch, clip_row, n, cpg,
+                       cpg_g_stride);
   else if (cis_dtype == LS_F16)
     hipLaunchKernelGGL(ls_nosa_cis_pages_kernel<LS_F16>, grid, dim3(256), 0, s,
-                       (const uint16_t*)cis, cis_rs, cu_k, cu_a, pg_off, batch, n, cpg, cpg_g_stride);
+                       (const uint16_t*)cis, cis_rs, cu_k, cu_a, pg_off, batch, clip_row, n, cpg,
+                       cpg_g_stride);
   else
     hipLaunchKernelGGL(ls_nosa_cis_pages_kernel<LS_F32>, grid, dim3(256), 0, s,
-                       (const float*)cis, cis_rs, cu_k, cu_a, pg_off, batch, n, cpg, cpg_g_stride);
+                       (const float*)cis, cis_rs, cu_k, cu_a, pg_off, batch, clip_row, n, cpg,
+                       cpg_g_stride);
   return ls_check_launch("ls_nosa_cis_pages_kernel");
 }
 
@@ -488,10 +502,12 @@ __device__ __forceinline__ void ls_nosa_topk_row(
 // p < out_len: -inf after q_idx, +inf forced, -inf without a CIS page score
 // (p > A_b / 4), else the float32 CIS page score; the n_order best (ties to
 // the lower page) are written best first to order[((g * n_blk + blk) * 2 + v)
-// * n_order + i] (entries past out_len pages stay -1).
+// * n_order + i] (entries past out_len pages stay -1).  Under
+// LS_POOL_CLIP_ROW the pages A_b / 4 < p <= A_max / 4 pool only padding
+// windows and score 0 (pages [n_scored, n_zero)).
 template <int NS>
 __device__ __forceinline__ void ls_nosa_rank_block(const float* __restrict__ cpg_seq, int n_scored,
-                                                   int out_len, int off_bq, int q_idx,
+                                                   int n_zero, int out_len, int off_bq, int q_idx,
                                                    int init_blocks, int local_blocks, int n_order,
                                                    int lane, int32_t* __restrict__ out,
                                                    uint32_t* __restrict__ scr,
@@ -499,6 +515,7 @@ __device__ __forceinline__ void ls_nosa_rank_block(const float* __restrict__ cpg
                                                    int32_t* __restrict__ s_page) {
   constexpr int NW = (NS + 31) / 32;
   const uint32_t pinf = ls_order_key32(0x7f800000u), ninf = ls_order_key32(0xff800000u);
+  const uint32_t zero = ls_order_key32(0u);
   uint32_t key[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
@@ -507,7 +524,8 @@ __device__ __forceinline__ void ls_nosa_rank_block(const float* __restrict__ cpg
     if (p >= out_len) k = 0u;
     else if (p > q_idx) k = ninf;
     else if (p < init_blocks || (off_bq - local_blocks <= p && p <= off_bq)) k = pinf;
-    else if (p >= n_scored) k = ninf;
+    else if (p >= n_zero) k = ninf;
+    else if (p >= n_scored) k = zero;
     else k = ls_order_key32(__builtin_bit_cast(uint32_t, cpg_seq[p]));
     key[s] = k;
   }
@@ -552,7 +570,8 @@ __global__ __launch_bounds__(64) void ls_nosa_cis_rank_kernel(
     const float* __restrict__ cpg, int64_t cpg_g_stride, const int32_t* __restrict__ pg_off,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_a,
     const int32_t* __restrict__ blk_off, int batch, int64_t n_blk, int max_seqlen_q, int out_len,
-    int init_blocks, int local_blocks, int block_size, int n_order, int32_t* __restrict__ order) {
+    int init_blocks, int local_blocks, int block_size, int clip_row, int n_order,
+    int32_t* __restrict__ order) {
   __shared__ uint32_t s_scr[256];
   __shared__ uint32_t s_key[LS_NOSA_MAX_ORDER];
   __shared__ int32_t s_page[LS_NOSA_MAX_ORDER];
@@ -569,10 +588,13 @@ __global__ __launch_bounds__(64) void ls_nosa_cis_rank_kernel(
   if (v == 1 && (t_last + max_seqlen_q - lq) / block_size == qa) return;  // one q_idx only
   const int A = cu_a[b + 1] - cu_a[b];
   const int n_scored = min(A > 0 ? A / 4 + 1 : 0, out_len);
+  const int a_max = pg_off[batch + 1];
+  const int n_zero = clip_row ? min(a_max > 0 ? a_max / 4 + 1 : 0, out_len) : n_scored;
   const float* cpg_seq = cpg + (int64_t)g * cpg_g_stride + pg_off[b];
   const int n_slots = (out_len + 63) >> 6;
-#define LS_RANK(NSV) ls_nosa_rank_block<NSV>(cpg_seq, n_scored, out_len, j, qa + v, init_blocks, \
-                                             local_blocks, n_order, lane, out, s_scr, s_key, s_page)
+#define LS_RANK(NSV) ls_nosa_rank_block<NSV>(cpg_seq, n_scored, n_zero, out_len, j, qa + v,     \
+                                             init_blocks, local_blocks, n_order, lane, out,     \
+                                             s_scr, s_key, s_page)
   if (n_slots <= 1) return LS_RANK(1);
   if (n_slots <= 4 || KPL <= 4) return LS_RANK(KPL < 4 ? KPL : 4);
   if (n_slots <= 16 || KPL <= 16) return LS_RANK(KPL < 16 ? KPL : 16);
@@ -635,7 +657,8 @@ static int launch_nosa_topk_k(int out_len, hipStream_t s, const void* P, int64_t
                               const int32_t* cu_q, const int32_t* cu_a, const int32_t* blk_off,
                               int64_t n_blk, int batch, int64_t total_q, int G, int max_q,
                               int init, int local, int qk_select, int take, int bs,
-                              uint32_t pinf1, uint32_t ninf1, int32_t* order, int32_t* out) {
+                              int clip_row, uint32_t pinf1, uint32_t ninf1, int32_t* order,
+                              int32_t* out) {
   const int n_order = take + qk_select;
   const dim3 rgrid((unsigned)n_blk, G, 2);
   const dim3 grid((unsigned)(((int64_t)G * total_q + 3) / 4));
@@ -643,7 +666,7 @@ static int launch_nosa_topk_k(int out_len, hipStream_t s, const void* P, int64_t
   do {                                                                                         \
     hipLaunchKernelGGL((ls_nosa_cis_rank_kernel<K>), rgrid, dim3(64), 0, s, cpg, cs, pg_off,   \
                        cu_q, cu_a, blk_off, batch, n_blk, max_q, out_len, init, local, bs,    \
-                       n_order, order);                                                        \
+                       clip_row, n_order, order);                                              \
     if (int rc = ls_check_launch("ls_nosa_cis_rank_kernel")) return rc;                       \
     hipLaunchKernelGGL((ls_nosa_topk_kernel<K, KEY32>), grid, dim3(256), 0, s, P, ps, cu_q,   \
                        cu_a, blk_off, batch, total_q, G, max_q, out_len, init, local,         \
@@ -664,15 +687,15 @@ int ls_nosa_topk_launch(int p_dtype, int out_len, const void* P, int64_t p_strid
                         const int32_t* cu_a, const int32_t* blk_off, int64_t n_blk, int batch,
                         int64_t total_q, int G, int max_seqlen_q, int init_blocks,
                         int local_blocks, int qk_select, int take, int block_size,
-                        int32_t* order, int32_t* topk_idx, hipStream_t s) {
+                        int clip_row, int32_t* order, int32_t* topk_idx, hipStream_t s) {
   if (total_q == 0 || G == 0 || take == 0) return LS_OK;
   if (take + qk_select > LS_NOSA_MAX_ORDER)
     return ls_fail(LS_ERR_UNSUPPORTED, "NOSA selection: topk + init + local + select blocks "
                    "above %d", LS_NOSA_MAX_ORDER);
 #define LS_NOSA_TOPK_ARGS                                                                      \
   out_len, s, P, p_stride, cpg, cpg_g_stride, pg_off, cu_q, cu_a, blk_off, n_blk, batch,     \
-      total_q, G, max_seqlen_q, init_blocks, local_blocks, qk_select, take, block_size, pinf, \
-      ninf, order, topk_idx
+      total_q, G, max_seqlen_q, init_blocks, local_blocks, qk_select, take, block_size,       \
+      clip_row, pinf, ninf, order, topk_idx
   if (p_dtype == LS_F32) {
     const uint32_t pinf = ls_order_key32(0x7f800000u), ninf = ls_order_key32(0xff800000u);
     return launch_nosa_topk_k<true>(LS_NOSA_TOPK_ARGS);

@@ -4,11 +4,13 @@
 #include <hip/hip_runtime.h>
 #include <cstdint>
 
-// CIS page scores of every sequence: pg_off[b] (batch + 1 entries) and
-// cpg[g * cpg_g_stride + pg_off[b] + p] for p <= A_b / 4.
+// CIS page scores of every sequence: pg_off[b] (batch + 1 entries, then the
+// largest atom count A_max in pg_off[batch + 1]) and cpg[g * cpg_g_stride +
+// pg_off[b] + p] for p <= A_b / 4.  clip_row selects LS_POOL_CLIP_ROW.
 int ls_nosa_cis_pages_launch(const void* cis, int64_t cis_rs, int cis_dtype, const int32_t* cu_k,
                              const int32_t* cu_a, int batch, int64_t total_atoms, int G,
-                             int32_t* pg_off, float* cpg, int64_t cpg_g_stride, hipStream_t s);
+                             int clip_row, int32_t* pg_off, float* cpg, int64_t cpg_g_stride,
+                             hipStream_t s);
 
 // Two-stage NOSA top-k over the page-score scratch P ([G][total_q][p_stride]
 // of p_dtype, LS_F32 / LS_BF16 / LS_F16) and the CIS page scores (float32).
@@ -22,4 +24,4 @@ int ls_nosa_topk_launch(int p_dtype, int out_len, const void* P, int64_t p_strid
                         const int32_t* cu_a, const int32_t* blk_off, int64_t n_blk, int batch,
                         int64_t total_q, int G, int max_seqlen_q, int init_blocks,
                         int local_blocks, int qk_select, int take, int block_size,
-                        int32_t* order, int32_t* topk_idx, hipStream_t s);
+                        int clip_row, int32_t* order, int32_t* topk_idx, hipStream_t s);

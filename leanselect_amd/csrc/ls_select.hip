@@ -1015,7 +1015,7 @@ NosaWsLayout nosa_ws_layout(int64_t total_q, int64_t total_atoms, int batch, int
   NosaWsLayout N;
   N.L = ws_layout(total_q, total_atoms, batch, H, G, D, F, out_len, eb);
   size_t off = N.L.total;
-  N.pg = off; off += ls_align256((size_t)(batch + 1) * 4);
+  N.pg = off; off += ls_align256((size_t)(batch + 2) * 4);
   N.cpg_stride = (total_atoms / 4 + batch + 63) & ~(int64_t)63;
   N.cpg = off; off += ls_align256((size_t)G * N.cpg_stride * 4);
   // The query blocks' stage-2 page orders (64-row blocks: block_size 64).
@@ -1544,7 +1544,7 @@ extern "C" int ls_nosa_select_prefill(
     int32_t head_dim, const float* head_mix, const float* kv_head_mix, const float* q_proj,
     const float* k_proj, int32_t router_heads, int32_t router_dim, int32_t dtype, int32_t topk,
     int32_t block_size, int32_t kernel_stride, int32_t init_blocks, int32_t local_blocks,
-    int32_t select_blocks, int32_t* topk_idx, int32_t take, void* workspace,
+    int32_t select_blocks, int32_t pool_clip, int32_t* topk_idx, int32_t take, void* workspace,
     size_t workspace_bytes, void* stream) {
   int rc = check_dims("ls_nosa_select_prefill", num_heads, num_kv_heads, head_dim, router_heads,
                       router_dim, dtype);
@@ -1558,6 +1558,8 @@ extern "C" int ls_nosa_select_prefill(
              "ls_nosa_select_prefill: unknown CIS dtype %d", cis_dtype);
   LS_REQUIRE(init_blocks >= 0 && local_blocks >= 0 && select_blocks >= 0 && topk >= 0,
              LS_ERR_INVALID, "ls_nosa_select_prefill: block counts and topk must be >= 0");
+  LS_REQUIRE(pool_clip == LS_POOL_CLIP_SEQUENCE || pool_clip == LS_POOL_CLIP_ROW, LS_ERR_INVALID,
+             "ls_nosa_select_prefill: unknown pool_clip %d", pool_clip);
   const int out_len = (max_seqlen_q + block_size - 1) / block_size;
   const int want = topk < out_len ? topk : out_len;
   LS_REQUIRE(take == want, LS_ERR_INVALID,
@@ -1604,10 +1606,11 @@ extern "C" int ls_nosa_select_prefill(
   int32_t* pg_off = (int32_t*)(ws + N.pg);
   float* cpg = (float*)(ws + N.cpg);
   if ((rc = ls_nosa_cis_pages_launch(cis, cis_row_stride, cis_dtype, cu_seqlens_k, cu_seqlens_kc,
-                                     batch, total_atoms, G, pg_off, cpg, N.cpg_stride, s)))
+                                     batch, total_atoms, G, pool_clip, pg_off, cpg,
+                                     N.cpg_stride, s)))
     return rc;
   return ls_nosa_topk_launch(dtype, out_len, ws + L.p, L.p_stride, cpg, N.cpg_stride, pg_off,
                              cu_seqlens_q, cu_seqlens_kc, blk, N.n_blk, batch, total_q, G,
                              max_seqlen_q, init_blocks, local_blocks, qk_select, take, block_size,
-                             (int32_t*)(ws + N.order), topk_idx, s);
+                             pool_clip, (int32_t*)(ws + N.order), topk_idx, s);
 }

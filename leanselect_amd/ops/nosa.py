@@ -36,6 +36,7 @@ def max_pooling_1d_varlen(
     stride: int = 16,
     buf: torch.Tensor | None = None,
     max_cache_len: int | None = None,
+    clip: str = "sequence",
 ) -> torch.Tensor:
     """``[num_heads, total_q, max_k] -> [num_heads, total_q, out_len]``,
     ``out_len = ceil((max_seqlen_q + max_cache_len) / block_size)``.
@@ -43,11 +44,15 @@ def max_pooling_1d_varlen(
     Page ``p`` of row ``t`` (sequence ``b``, page ``off = (t - cu_q[b] +
     cache_lens[b]) // block_size``) is ``+inf`` when ``p < init_blocks`` or
     ``off - local_blocks <= p <= off``, else the max of ``input[h, t, j]`` over
-    ``j in [p*s - 1, p*s + s)`` within the sequence's ``len_k`` columns
-    (``-inf`` when empty), ``s = block_size // stride``.
+    ``j in [p*s - 1, p*s + s)`` (``-inf`` when empty), ``s = block_size //
+    stride``, within the sequence's ``len_k`` columns (``clip="sequence"``) or
+    the row's ``max_seqlen_k`` columns (``clip="row"``).  The upstream kernel
+    body that fixes this choice is not in the reference tree; the two differ
+    only where a shorter sequence's padding columns hold values above -inf.
     """
     if input.ndim != 3:
         raise ValueError(f"Expected 3D input, got {input.ndim}D")
+    clip_code = _hip.pool_clip_code(clip)
     for name, t in (("cu_seqlens_q", cu_seqlens_q), ("cu_seqlens_k", cu_seqlens_k),
                     ("cache_lens", cache_lens)):
         if t.dtype != torch.int32:
@@ -77,7 +82,7 @@ def max_pooling_1d_varlen(
         input.data_ptr(), cu_seqlens_q.contiguous().data_ptr(),
         cu_seqlens_k.contiguous().data_ptr(), cache_lens.contiguous().data_ptr(), batch, H,
         total_q, int(max_seqlen_k), out_len, int(local_blocks), int(init_blocks), block_size,
-        stride, _hip.dtype_code(input.dtype), out.data_ptr(), _hip.stream_of(dev))
+        stride, clip_code, _hip.dtype_code(input.dtype), out.data_ptr(), _hip.stream_of(dev))
     _hip.check(rc, "ls_page_maxpool_varlen")
     return out
 
@@ -107,6 +112,7 @@ def nosa_prefill_topk_idx(
     kernel_stride: int = 16,
     max_seqlen_q: int | None = None,
     cu_seqlens_q_host: list[int] | None = None,
+    pool_clip: str = "sequence",
 ) -> torch.Tensor:
     """NOSA page plans ``[G, total_q, min(topk, ceil(max_seqlen_q / block_size))]`` int32.
 
@@ -115,9 +121,14 @@ def nosa_prefill_topk_idx(
     eviction scores of the original keys (prefix offsets ``cu_seqlens_k``),
     ``selector`` a ``LeanSelectSelector``.  Rows list their pages ascending;
     pages after the row's ``q_idx`` (aligned to the longest sequence) are -1.
+    ``pool_clip`` is the column range of both page max-pools (see
+    ``max_pooling_1d_varlen``): under ``"row"`` a shorter sequence's pages past
+    its own windows pool the CIS means' zero padding, up to the longest
+    sequence's window count.
     """
     if q_unpad.ndim != 3 or k_compressed.ndim != 3:
         raise ValueError("q_unpad must be [total_q, H, D] and k_compressed [A, G, D]")
+    clip_code = _hip.pool_clip_code(pool_clip)
     dev = _hip.require_gpu(q_unpad, k_compressed, cis, cu_seqlens_q, cu_seqlens_kc, cu_seqlens_k)
     for t in (cu_seqlens_q, cu_seqlens_kc, cu_seqlens_k):
         if t.dtype != torch.int32:
@@ -158,7 +169,7 @@ def nosa_prefill_topk_idx(
         cu_seqlens_k.contiguous().data_ptr(), batch, int(max_seqlen_q), H, G, D,
         hm.data_ptr(), khm.data_ptr(), qp.data_ptr(), kp.data_ptr(), selector.router_heads,
         selector.router_dim, dt, int(topk), block_size, kernel_stride, int(init_blocks),
-        int(local_blocks), int(select_blocks), topk_idx.data_ptr(), take, ws.data_ptr(),
+        int(local_blocks), int(select_blocks), clip_code, topk_idx.data_ptr(), take, ws.data_ptr(),
         ws.numel(), _hip.stream_of(dev))
     _hip.check(rc, "ls_nosa_select_prefill")
     return topk_idx

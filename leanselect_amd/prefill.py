@@ -90,11 +90,14 @@ def nosa_sparse_prefill(
     kernel_stride: int = 16,
     cu_seqlens_host: list[int] | None = None,
     return_topk_idx: bool = False,
+    pool_clip: str = "sequence",
 ):
     """``(out [total, H, D], topk_idx [G, total, take])`` of a NOSA layer.
 
     ``cis [total, G]`` are the per-token eviction scores.  The selection scores
     the post-RoPE queries, as the LeanSelect branch does (nosa.py:2011-2019).
+    ``pool_clip`` is the page max-pool's column range (``"sequence"`` or
+    ``"row"``, as in ``nosa_prefill_topk_idx``).
     """
     host = cu_seqlens_host if cu_seqlens_host is not None else cu_seqlens.tolist()
     max_len = max(host[i + 1] - host[i] for i in range(len(host) - 1))
@@ -107,7 +110,7 @@ def nosa_sparse_prefill(
         q, kc, cis, cu_seqlens, cu_c, cu_seqlens, selector,
         topk=topk, init_blocks=init_blocks, local_blocks=local_blocks,
         select_blocks=select_blocks, block_size=block_size, kernel_stride=kernel_stride,
-        max_seqlen_q=max_len, cu_seqlens_q_host=host)
+        max_seqlen_q=max_len, cu_seqlens_q_host=host, pool_clip=pool_clip)
     range_pop()
     range_push("stage 2")
     out = nosa_sparse_attention(q, k, v, cis, cu_seqlens, cu_seqlens, max_len, max_len, ids,

@@ -11,7 +11,11 @@ Restated reference code (paths relative to the LeanSelect repository root):
   the one the reference restates in ``leanselect/baselines/page_topk.py:4-26,
   94-117``: page ``p`` pools window ``[p*s - 1, p*s + s)`` (``s = block_size /
   stride``), sink pages and the ``local_blocks + 1`` pages ending at the row's
-  page are ``+inf``.  Parity of that kernel is unpinned beyond this contract.
+  page are ``+inf``.  Parity of that kernel is unpinned beyond this contract,
+  and the contract leaves one choice open: whether a row pools only its own
+  sequence's ``cu_seqlens_k`` columns or the whole padded row of
+  ``max_seqlen_k`` columns.  Both are kept (``clip="sequence"`` / ``"row"``),
+  each pinned against a brute-force loop.
 * ``leanselect/models/nosa.py:1144-1307`` -- ``compressed_attention`` with
   ``precomputed_qk_score`` (the LeanSelect branch, ``nosa.py:2071-2098``), and
   ``nosa.py:1822-1853`` -- ``_leanselect_atom_scores``.
@@ -105,6 +109,11 @@ def _pool_pages(x: torch.Tensor, lk: int, out_len: int, s: int) -> torch.Tensor:
     return g.masked_fill(~valid, float("-inf")).amax(dim=-1)
 
 
+def _check_clip(clip: str) -> None:
+    if clip not in ("sequence", "row"):
+        raise ValueError(f"clip must be 'sequence' or 'row', got {clip!r}")
+
+
 def _forced(off_bq: torch.Tensor, out_len: int, init_blocks: int, local_blocks: int) -> torch.Tensor:
     """Sink pages and the ``local_blocks + 1`` pages ending at ``off_bq``, ``[n, out_len]``."""
     pages = torch.arange(out_len)[None, :]
@@ -123,6 +132,7 @@ def page_maxpool_varlen(
     init_blocks: int,
     block_size: int = 64,
     stride: int = 16,
+    clip: str = "sequence",
 ) -> torch.Tensor:
     """``[Hk, total_q, max_k] -> [Hk, total_q, out_len]`` page max with the forced overlay.
 
@@ -131,10 +141,13 @@ def page_maxpool_varlen(
     block_size``.  Page ``p`` is ``+inf`` when ``p < init_blocks`` or
     ``off_bq - local_blocks <= p <= off_bq``, else the max of
     ``inp[h, t, j]`` over ``j in [p*s - 1, p*s + s)`` clipped to the
-    sequence's ``len_k(b)`` score columns (``-inf`` when empty).  The clip to
-    ``len_k(b)`` rather than ``max_k`` is this restatement's choice (unpinned);
-    it matters only where a shorter sequence's columns hold zeros.
+    sequence's ``len_k(b)`` score columns (``clip="sequence"``) or to the row's
+    ``max_k`` columns (``clip="row"``), ``-inf`` when empty.  Which of the two
+    the upstream kernel applies is not fixed by the reference tree (its body is
+    un-vendored); both are kept, and they differ only where a shorter
+    sequence's padding columns hold values above ``-inf``.
     """
+    _check_clip(clip)
     cq = _as_list(cu_seqlens_q)
     ck = _as_list(cu_seqlens_k)
     cl = _as_list(cache_lens)
@@ -147,7 +160,8 @@ def page_maxpool_varlen(
         q0, q1 = cq[b], cq[b + 1]
         if q1 <= q0:
             continue
-        pooled = _pool_pages(x[:, q0:q1], min(ck[b + 1] - ck[b], max_k), out_len, s)
+        lk = max_k if clip == "row" else min(ck[b + 1] - ck[b], max_k)
+        pooled = _pool_pages(x[:, q0:q1], lk, out_len, s)
         off_bq = (torch.arange(q1 - q0) + cl[b]) // block_size
         out[:, q0:q1] = pooled.masked_fill(_forced(off_bq, out_len, init_blocks, local_blocks)[None],
                                            float("inf"))
@@ -205,6 +219,7 @@ def nosa_select_prefill(
     kernel_size: int = 32,
     rows: Sequence[int] | None = None,
     return_scores: bool = False,
+    clip: str = "sequence",
 ):
     """NOSA page plans ``[G, R, min(topk, out_len)]`` int32 (prefill).
 
@@ -217,7 +232,11 @@ def nosa_select_prefill(
     pages, sorted, with ids past the row's page replaced by ``-1``.  Ties go to
     the lower page (``torch.topk`` leaves them unspecified).  With
     ``return_scores`` the qk and (masked, overlaid) CIS page scores are returned.
+    ``clip`` is the pooling's column range (``page_maxpool_varlen``): the
+    sequence's ``len_kc(b)`` windows, or the rows' whole width (``max_kc``
+    atom columns, ``max_seqlen_k // 16 - 1`` window means whose padding is 0).
     """
+    _check_clip(clip)
     cq = _as_list(cu_seqlens_q)
     ckc = _as_list(cu_seqlens_kc)
     total_q = cq[-1]
@@ -241,8 +260,11 @@ def nosa_select_prefill(
                                          kernel_stride)
         forced = _forced(torch.tensor([(r - cq[b]) // block_size]), out_len, init_blocks,
                          local_blocks)[0]
-        pb = _pool_pages(atom_score[:, i].to(torch.float64), lk, out_len, s)
-        pc = _pool_pages(means[b].to(torch.float64), lk, out_len, s)
+        row_clip = clip == "row"
+        pb = _pool_pages(atom_score[:, i].to(torch.float64),
+                         atom_score.shape[-1] if row_clip else lk, out_len, s)
+        pc = _pool_pages(means[b].to(torch.float64), means[b].shape[-1] if row_clip else lk,
+                         out_len, s)
         block[:, i] = pb.masked_fill(forced[None], float("inf"))
         block_cis[:, i] = pc.masked_fill(forced[None], float("inf"))
     q_idx_all = nosa_q_idx(cq, max_seqlen_q, block_size)
@@ -276,12 +298,15 @@ def nosa_two_stage(block: torch.Tensor, block_cis: torch.Tensor, q_idx: torch.Te
 
 def nosa_pool_rows(page_qk: torch.Tensor, cis_means: torch.Tensor, cu_seqlens_q,
                    cu_seqlens_kc, rows: Sequence[int], *, out_len: int, init_blocks: int,
-                   local_blocks: int, block_size: int = 64, kernel_stride: int = 16):
+                   local_blocks: int, block_size: int = 64, kernel_stride: int = 16,
+                   clip: str = "sequence"):
     """Stage inputs of ``nosa_two_stage`` from given intermediate scores: qk page
     scores ``page_qk [G, R, >= out_len]`` (pages without atoms ``-inf``) and
     pooled CIS window means ``cis_means [G, total_q, M]`` (``nosa_mean_pooling``
-    layout), with the forced overlay of ``max_pooling_1d_varlen``.  Returns
-    ``(block, block_cis)`` ``[G, R, out_len]`` float64."""
+    layout), with the forced overlay of ``max_pooling_1d_varlen`` and its
+    ``clip`` (the CIS means pool the sequence's windows, or all ``M``).
+    Returns ``(block, block_cis)`` ``[G, R, out_len]`` float64."""
+    _check_clip(clip)
     cq = _as_list(cu_seqlens_q)
     ckc = _as_list(cu_seqlens_kc)
     s = block_size // kernel_stride
@@ -297,7 +322,8 @@ def nosa_pool_rows(page_qk: torch.Tensor, cis_means: torch.Tensor, cu_seqlens_q,
         n = min(out_len, page_qk.shape[-1])
         pb = torch.full((G, out_len), float("-inf"), dtype=torch.float64)
         pb[:, :n] = page_qk[:, i, :n].to(torch.float64)
-        pc = _pool_pages(cis_means[:, r].to(torch.float64), lk, out_len, s)
+        pc = _pool_pages(cis_means[:, r].to(torch.float64),
+                         cis_means.shape[-1] if clip == "row" else lk, out_len, s)
         block[:, i] = pb.masked_fill(forced[None], float("inf"))
         block_cis[:, i] = pc.masked_fill(forced[None], float("inf"))
     return block, block_cis

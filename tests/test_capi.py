@@ -59,16 +59,20 @@ def test_nosa_entry_points_validate_before_any_launch():
     # take must be min(topk, ceil(max_seqlen_q / 64)) = 2 for 100 tokens.
     rc = lib.ls_nosa_select_prefill(None, 0, 100, None, 0, 5, None, 0, B, None, None, None, 1,
                                     100, 32, 2, 128, None, None, None, None, 4, 32, B, 96, 64, 16,
-                                    1, 16, 24, None, 3, None, 0, None)
+                                    1, 16, 24, 0, None, 3, None, 0, None)
     assert rc == _hip.LS_ERR_INVALID and b"take" in lib.ls_last_error()
     rc = lib.ls_nosa_select_prefill(None, 0, 100, None, 0, 5, None, 0, B, None, None, None, 1,
                                     100, 32, 2, 128, None, None, None, None, 4, 32, B, 96, 32, 16,
-                                    1, 16, 24, None, 2, None, 0, None)
+                                    1, 16, 24, 0, None, 2, None, 0, None)
     assert rc == _hip.LS_ERR_UNSUPPORTED and b"block_size" in lib.ls_last_error()
     rc = lib.ls_nosa_select_prefill(None, 0, 100, None, 0, 5, None, 0, 7, None, None, None, 1,
                                     100, 32, 2, 128, None, None, None, None, 4, 32, B, 96, 64, 16,
-                                    1, 16, 24, None, 2, None, 0, None)
+                                    1, 16, 24, 0, None, 2, None, 0, None)
     assert rc == _hip.LS_ERR_INVALID and b"CIS dtype" in lib.ls_last_error()
+    rc = lib.ls_nosa_select_prefill(None, 0, 100, None, 0, 5, None, 0, B, None, None, None, 1,
+                                    100, 32, 2, 128, None, None, None, None, 4, 32, B, 96, 64, 16,
+                                    1, 16, 24, 2, None, 2, None, 0, None)
+    assert rc == _hip.LS_ERR_INVALID and b"pool_clip" in lib.ls_last_error()
     rc = lib.ls_nosa_attn_varlen(None, 0, None, 0, None, 0, None, 0, B, None, None, 1, 10, 10,
                                  10, 10, 32, 2, 128, B, None, 1, 64, -1.0, None, None, None, 0,
                                  None)
@@ -81,12 +85,18 @@ def test_nosa_entry_points_validate_before_any_launch():
     assert rc == _hip.LS_ERR_UNSUPPORTED
     rc = lib.ls_cis_mean_pool(None, 1, 10, 2, None, 1, 100, 32, 16, B, None, 6, None)
     assert rc == _hip.LS_ERR_INVALID and b"columns" in lib.ls_last_error()
-    rc = lib.ls_page_maxpool_varlen(None, None, None, None, 1, 2, 10, 10, 1, 2, 1, 64, 16, 9,
+    rc = lib.ls_page_maxpool_varlen(None, None, None, None, 1, 2, 10, 10, 1, 2, 1, 64, 16, 0, 9,
                                     None, None)
     assert rc == _hip.LS_ERR_INVALID and b"dtype" in lib.ls_last_error()
-    rc = lib.ls_page_maxpool_varlen(None, None, None, None, 1, 2, 10, 10, 1, 2, 1, 64, 48, B,
+    rc = lib.ls_page_maxpool_varlen(None, None, None, None, 1, 2, 10, 10, 1, 2, 1, 64, 48, 0, B,
                                     None, None)
     assert rc == _hip.LS_ERR_INVALID
+    rc = lib.ls_page_maxpool_varlen(None, None, None, None, 1, 2, 10, 10, 1, 2, 1, 64, 16, 2, B,
+                                    None, None)
+    assert rc == _hip.LS_ERR_INVALID and b"clip" in lib.ls_last_error()
+    assert (_hip.LS_POOL_CLIP_SEQUENCE, _hip.LS_POOL_CLIP_ROW) == (0, 1)
+    with pytest.raises(ValueError, match="clip"):
+        _hip.pool_clip_code("max_k")
 
 
 def test_nosa_workspace_and_cpu_refusal():

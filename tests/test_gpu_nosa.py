@@ -53,8 +53,12 @@ def test_cis_mean_pooling(dtype):
         assert bool((got[:, cu[b] : cu[b + 1], m_fit:] == 0).all())
 
 
+@pytest.mark.parametrize("clip", ["sequence", "row"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-def test_page_maxpool_varlen_exact(dtype):
+def test_page_maxpool_varlen_exact(dtype, clip):
+    """Every score column holds a value (the padding too), so the two clips
+    give different pages wherever a shorter sequence's window reaches past its
+    columns."""
     lens_q, lens_k, cache = [700, 1, 130, 2000], [40, 0, 7, 124], [0, 128, 5, 0]
     cq, ck = [0], [0]
     for a, b in zip(lens_q, lens_k):
@@ -63,13 +67,16 @@ def test_page_maxpool_varlen_exact(dtype):
     max_k = max(lens_k)
     g = torch.Generator(device="cpu").manual_seed(3)
     inp = torch.randn(2, cq[-1], max_k, generator=g).to(dtype)
-    args = dict(local_blocks=3, init_blocks=2, block_size=64, stride=16)
+    args = dict(local_blocks=3, init_blocks=2, block_size=64, stride=16, clip=clip)
     t = lambda x: torch.tensor(x, dtype=torch.int32, device=DEV)  # noqa: E731
     got = max_pooling_1d_varlen(inp.to(DEV), t(cq), t(ck), t(cache), max(lens_q), max_k,
                                 **args).cpu()
     want = oracle.page_maxpool_varlen(inp, cq, ck, cache, max(lens_q), max_k, **args)
     assert got.shape == want.shape
     assert torch.equal(got.double(), want.double())
+    other = oracle.page_maxpool_varlen(inp, cq, ck, cache, max(lens_q), max_k,
+                                       **{**args, "clip": "row" if clip == "sequence" else "sequence"})
+    assert not torch.equal(got.double(), other.double())
     buf = torch.empty_like(got, device=DEV)
     got2 = max_pooling_1d_varlen(inp.to(DEV), t(cq), t(ck), t(cache), max(lens_q), max_k,
                                  buf=buf, **args)
@@ -105,9 +112,10 @@ def _gpu_page_scores(case, kc, cu_c_host, rows, out_len):
     return res
 
 
-def _check_nosa_select(case, cis, rows, *, topk, init, local, select, max_band_rows=0):
+def _check_nosa_select(case, cis, rows, *, topk, init, local, select, max_band_rows=0,
+                       clip="sequence"):
     kc, cu_c, ids = _nosa_select(case, cis, topk=topk, init_blocks=init, local_blocks=local,
-                                 select_blocks=select)
+                                 select_blocks=select, pool_clip=clip)
     cu = case.cu_host
     max_q = case.max_seqlen
     out_len = (max_q + 63) // 64
@@ -121,7 +129,7 @@ def _check_nosa_select(case, cis, rows, *, topk, init, local, select, max_band_r
     means = nosa_mean_pooling(cis.to(DEV), case.cu_seqlens, max_q).cpu()
     block, block_cis = oracle.nosa_pool_rows(page_qk, means, cu, cu_c_host, rows,
                                              out_len=out_len, init_blocks=init,
-                                             local_blocks=local)
+                                             local_blocks=local, clip=clip)
     want_same = oracle.nosa_two_stage(block, block_cis, q_idx, topk=topk,
                                       qk_select=init + local + select)
     diff = (got != want_same).any(-1)
@@ -133,7 +141,7 @@ def _check_nosa_select(case, cis, rows, *, topk, init, local, select, max_band_r
     atom = oracle.nosa_atom_scores(case.q.cpu(), kc.cpu(), cu, cu_c_host, qf, kf, rows=rows)
     want, blk, over = oracle.nosa_select_prefill(
         atom, cis, cu, cu_c_host, cu, max_q, max_q, topk=topk, init_blocks=init,
-        local_blocks=local, select_blocks=select, rows=rows, return_scores=True)
+        local_blocks=local, select_blocks=select, rows=rows, return_scores=True, clip=clip)
     rep = oracle.check_nosa_topk(got, want, blk, over, topk=topk, qk_select=init + local + select)
     print(f"\nNOSA selection vs independent oracle: {rep}")
     assert rep.ok, str(rep)
@@ -149,15 +157,22 @@ def test_nosa_select_10k_paper_budget():
     _check_nosa_select(case, cis, rows, topk=96, init=1, local=16, select=24)
 
 
-def test_nosa_select_ragged_q_idx_alignment():
+@pytest.mark.parametrize("clip", ["sequence", "row"])
+def test_nosa_select_ragged_q_idx_alignment(clip):
     """Shorter sequences' q_idx is right-aligned to the longest one: their late
-    pages pass the q_idx mask, and -1 fills the ids past it."""
+    pages pass the q_idx mask, and -1 fills the ids past it.  Under the row
+    clip those late pages pool the CIS means' zero padding (score 0, above
+    about half of the real pages), so the two clips choose different pages."""
     lens = (3000, 700, 31, 4500, 64)
     case = workloads.hidden_space_layer(lens, device=DEV, seed=12)
     cis = _cis(sum(lens), 2, seed=12)
     rows = spread_rows(case.cu_host, per_seq=64)
-    ids = _check_nosa_select(case, cis, rows, topk=12, init=1, local=2, select=3)
+    ids = _check_nosa_select(case, cis, rows, topk=12, init=1, local=2, select=3, clip=clip)
     assert ids.shape == (2, sum(lens), 12)
+    if clip == "row":
+        _, _, seq_ids = _nosa_select(case, cis, topk=12, init_blocks=1, local_blocks=2,
+                                     select_blocks=3)
+        assert not torch.equal(ids.cpu(), seq_ids.cpu())
 
 
 def test_nosa_select_fp32_and_fp16():
@@ -182,12 +197,14 @@ def test_nosa_select_tied_cis_scores():
 # ---------------------------------------------------------------------------
 # CIS-biased attention
 # ---------------------------------------------------------------------------
-def test_nosa_select_batch_without_any_compressed_key():
+@pytest.mark.parametrize("clip", ["sequence", "row"])
+def test_nosa_select_batch_without_any_compressed_key(clip):
     """No compressed key in the whole batch: the plans are the forced pages only."""
     lens = (20, 3, 31)
     case = workloads.hidden_space_layer(lens, device=DEV, seed=21)
     cis = _cis(sum(lens), 2, seed=21)
-    _check_nosa_select(case, cis, list(range(sum(lens))), topk=8, init=1, local=2, select=2)
+    _check_nosa_select(case, cis, list(range(sum(lens))), topk=8, init=1, local=2, select=2,
+                       clip=clip)
 
 
 def _check_nosa_attention(case, cis, ids, rows, **kw):

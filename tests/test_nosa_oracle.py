@@ -82,9 +82,10 @@ def _select_loop(block_row, cis_row, q_idx, topk, n_short):
     return [(-1 if p > q_idx else p) for p in ids]
 
 
-def test_nosa_selection_loop_restatement():
+@pytest.mark.parametrize("clip", ["sequence", "row"])
+def test_nosa_selection_loop_restatement(clip):
     torch.manual_seed(2)
-    lens = [700, 131]
+    lens = [2000, 700]  # the short sequence has 11 pages of real windows
     cq = _cu(lens)
     ck = _cu([(n - 32) // 16 + 1 for n in lens])
     G, max_kc = 2, int((ck[1:] - ck[:-1]).max())
@@ -94,19 +95,29 @@ def test_nosa_selection_loop_restatement():
     cis = torch.randn(sum(lens), G).to(torch.bfloat16)
     ids, block, over = oracle.nosa_select_prefill(
         atom, cis, cq, ck, cq, max(lens), max(lens), topk=12, init_blocks=1, local_blocks=2,
-        select_blocks=3, return_scores=True)
+        select_blocks=3, return_scores=True, clip=clip)
     q_idx = oracle.nosa_q_idx(cq, max(lens))
     score_cis = oracle.nosa_mean_pooling(cis, cq, max(lens))
     out_len = (max(lens) + 63) // 64
+    n_differ = 0
     for r in range(0, sum(lens), 7):
         b = 0 if r < lens[0] else 1
         lk = int(ck[b + 1] - ck[b])
         off = (r - int(cq[b])) // 64
         for g in range(G):
-            brow = _pool_loop(atom[g, r].tolist(), lk, out_len, off, 1, 2)
-            crow = _pool_loop(score_cis[g, r].double().tolist(), lk, out_len, off, 1, 2)
+            # The row clip pools the padded row: max_kc atom columns (-inf padding)
+            # and max(lens) // 16 - 1 window means (0 padding).
+            lk_qk = max_kc if clip == "row" else lk
+            lk_cis = score_cis.shape[-1] if clip == "row" else lk
+            brow = _pool_loop(atom[g, r].tolist(), lk_qk, out_len, off, 1, 2)
+            crow = _pool_loop(score_cis[g, r].double().tolist(), lk_cis, out_len, off, 1, 2)
             want = _select_loop(brow, crow, int(q_idx[r]), 12, 1 + 2 + 3)
             assert ids[g, r].tolist() == want, (r, g)
+            if clip == "row":
+                crow_seq = _pool_loop(score_cis[g, r].double().tolist(), lk, out_len, off, 1, 2)
+                n_differ += want != _select_loop(brow, crow_seq, int(q_idx[r]), 12, 1 + 2 + 3)
+    if clip == "row":  # the short sequence's late pages score 0 instead of -inf
+        assert n_differ > 0
 
 
 def test_nosa_attention_is_numerator_over_denominator():
@@ -175,6 +186,14 @@ def test_page_pooling_clips_to_each_sequence_and_the_choice_is_visible():
     assert got[0, t].tolist() == own
     assert own != padded  # page 2 reads column 9 under the max_k clip
     assert own[2] == -5.0 and padded[2] == 7.0 and own[3] == -math.inf
+    # clip="row" is the padded loop; for the longest sequence both clips agree.
+    got_row = oracle.page_maxpool_varlen(inp, cq, ck, torch.zeros(2, dtype=torch.int32), 300,
+                                         max_k, local_blocks=0, init_blocks=0, clip="row")
+    assert got_row[0, t].tolist() == padded
+    assert torch.equal(got_row[:, 300:], got[:, 300:])
+    with pytest.raises(ValueError, match="clip"):
+        oracle.page_maxpool_varlen(inp, cq, ck, torch.zeros(2, dtype=torch.int32), 300, max_k,
+                                   local_blocks=0, init_blocks=0, clip="max_k")
 
 
 def test_nosa_checker_flags_differences_without_a_tie():
