@@ -175,6 +175,29 @@ def test_nosa_select_ragged_q_idx_alignment(clip):
         assert not torch.equal(ids.cpu(), seq_ids.cpu())
 
 
+def test_nosa_select_with_nan_and_inf_scores():
+    """NaN and infinities in the qk scores.  NOSA's selection has no -1 rule for
+    them (nosa.py:1288-1305: only ids past q_idx become -1): ``torch.topk``
+    ranks NaN above +inf, so NaN pages enter the shortlist first (ties to the
+    lower page) and are then chosen at +inf in stage 2.  Planted in query rows
+    (every page of the row's group scores NaN, or mixes +-inf) and in key rows
+    (the pages around one window score NaN for every row)."""
+    import dataclasses
+    case = workloads.hidden_space_layer((6000,), device=DEV, seed=16)
+    q, k = case.q.clone(), case.k.clone()
+    nan, inf = float("nan"), float("inf")
+    for r, h, d, val in ((700, 3, 5, nan), (2600, 20, 9, nan), (4100, 5, 77, inf),
+                         (5100, 21, 3, -inf)):
+        q[r, h, d] = val
+    k[64 * 30 + 7, 1, 9] = nan
+    k[64 * 50 + 2, 0, 4] = inf
+    case = dataclasses.replace(case, q=q, k=k)
+    cis = _cis(6000, 2, seed=16)
+    rows = sorted(set(spread_rows(case.cu_host, per_seq=64)) | {700, 2600, 4100, 5100, 64 * 31,
+                                                                64 * 51 + 3})
+    _check_nosa_select(case, cis, rows, topk=24, init=1, local=4, select=6)
+
+
 def test_nosa_select_fp32_and_fp16():
     case = workloads.head_space_layer(5000, device=DEV, seed=13)
     cis = _cis(5000, 2, torch.float32, seed=13)
