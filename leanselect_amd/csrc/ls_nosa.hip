@@ -330,6 +330,157 @@ __device__ __forceinline__ int ls_nosa_mark_packed(uint32_t* __restrict__ scr, i
   return n_sel;
 }
 
+// Stage 1 of a row of bf16 page scores through a fast path: the shortlist S =
+// every forced page plus the kq - F best other pages (F forced pages), valid
+// when no loaded score is NaN or +inf (then nothing ties with the forced
+// pages' +inf) and the kq-th largest of the lanes' two largest scores, lo, is
+// positive.  The row is read through a buffer resource bounded at the scored
+// columns (reads past them return +0, which a positive lo leaves out), scores
+// are compared as float32, and the scores >= lo are gathered as raw bits << 16
+// | page in page order (at most 256).  lo is a lower bound of the (kq - F)-th
+// best non-forced score: of the kq largest among the lanes' top two (values of
+// distinct pages), at most F are forced pages.  The gathered non-forced
+// entries then hold every non-forced score >= lo; their (kq - F)-th largest
+// order key T is bisected, and the pages above T plus the lowest pages at T
+// are marked with the forced ones in the page bitmap that replaces the
+// scratch.  Returns |S| (= kq), or -1 (nothing marked) when the row needs the
+// general path.
+template <int NP>
+__device__ __forceinline__ int ls_nosa_stage1_finish(uint32_t* __restrict__ scr, int n,
+                                                     uint32_t lo, int kq, int k2, int lo_end,
+                                                     int la, int lb, int n_words, int lane) {
+  uint32_t pk[NP];
+  uint32_t hk = 0u;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const bool valid = i * 64 + lane < n;
+    const uint32_t e = valid ? scr[i * 64 + lane] : 0u;
+    const int page = (int)(e & 0xffffu);
+    const bool forced = page < lo_end || (page >= la && page <= lb);
+    // Positive bf16 scores: bf16 | 0x8000 is the order key.
+    pk[i] = valid && !forced ? (e | 0x80000000u) : 0u;
+    hk = max(hk, pk[i] >> 16);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) hk = max(hk, (uint32_t)__shfl_xor((int)hk, o, LS_WAVE));
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)hk);
+  uint32_t T = lo;
+  const uint32_t d = lo ^ hi;
+  if (d != 0u) {
+    const int tb = 31 - __builtin_clz(d);
+    T = lo & ~((2u << tb) - 1u);
+#pragma unroll 1
+    for (int bit = tb; bit >= 0; --bit) {
+      const uint32_t cand = (T | (1u << bit)) << 16;
+      int cnt = 0;
+#pragma unroll
+      for (int i = 0; i < NP; ++i) cnt += __popcll(__ballot(pk[i] >= cand));
+      if (cnt >= k2) T |= 1u << bit;
+    }
+  }
+  const uint32_t above = (T << 16) | 0xffffu;
+  int gt = 0;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) gt += __popcll(__ballot(pk[i] > above));
+  const int m = k2 - gt;
+  // Every lane has read its entries: the scratch becomes the bitmap.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (int i = lane; i < n_words; i += 64) scr[i] = 0u;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int eq_before = 0;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const bool eq = pk[i] != 0u && (pk[i] >> 16) == T;
+    const uint64_t eq_mask = __ballot(eq);
+    const int eq_rank = eq_before + ls_lanes_below(eq_mask);
+    if (pk[i] > above || (eq && eq_rank < m)) {
+      const uint32_t page = pk[i] & 0xffffu;
+      atomicOr(&scr[page >> 5], 1u << (page & 31));
+    }
+    eq_before += __popcll(eq_mask);
+  }
+  const int nf = kq - k2;
+  for (int i = lane; i < nf; i += 64) {
+    const int page = i < lo_end ? i : la + (i - lo_end);
+    atomicOr(&scr[page >> 5], 1u << (page & 31));
+  }
+  return kq;
+}
+
+template <int NS>
+__device__ __forceinline__ int ls_nosa_stage1_bf16(const uint16_t* __restrict__ row, int n_scored,
+                                                   int out_len, int off_bq, int init_blocks,
+                                                   int local_blocks, int kq, int n_words,
+                                                   int lane, uint32_t* __restrict__ scr) {
+  if (kq < 1 || kq > 128) return -1;
+  const int lo_end = min(init_blocks, out_len);
+  const int la = max(off_bq - local_blocks, lo_end), lb = min(off_bq, out_len - 1);
+  const int nf = lo_end + max(0, lb - la + 1);  // forced pages
+  if (nf >= kq) return -1;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)row, (short)0, n_scored * 2, 0x00020000);
+  uint32_t f[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    // The whole byte offset in a lane register (none of it in the scalar
+    // offset, which the hardware range check leaves out).
+    uint32_t off = (uint32_t)(lane * 2 + 128 * s);
+    asm("" : "+v"(off));
+    f[s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)off, 0, 0) << 16;
+  }
+  float m1 = -INFINITY, m2 = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const float x = __uint_as_float(f[s]);
+    m2 = __builtin_amdgcn_fmed3f(m1, m2, x);
+    m1 = __builtin_elementwise_maximum(m1, x);
+  }
+  if (__ballot(__builtin_isnan(m1) || m1 == INFINITY) != 0ull) return -1;
+  const uint32_t k1 = ls_order_key16((uint16_t)(__float_as_uint(m1) >> 16));
+  const uint32_t kb = ls_order_key16((uint16_t)(__float_as_uint(m2) >> 16));
+  uint32_t kmin = kb, kmax = k1;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, LS_WAVE));
+    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, LS_WAVE));
+  }
+  kmin = (uint32_t)__builtin_amdgcn_readfirstlane((int)kmin);
+  kmax = (uint32_t)__builtin_amdgcn_readfirstlane((int)kmax);
+  const uint32_t dk = kmin ^ kmax;
+  const int top = dk ? 31 - __builtin_clz(dk) : -1;
+  uint32_t lo = top >= 0 ? kmin & ~((2u << top) - 1u) : kmin;
+#pragma unroll
+  for (int bit = 15; bit >= 0; --bit) {
+    if (bit <= top) {
+      const uint32_t cand = lo | (1u << bit);
+      const int cnt = __popcll(__ballot(k1 >= cand)) + __popcll(__ballot(kb >= cand));
+      lo = cnt >= kq ? cand : lo;
+    }
+  }
+  if (lo <= 0x8000u) return -1;  // the bound must be a positive score
+  const float lo_f = __uint_as_float((lo & 0x7fffu) << 16);
+  int n = 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool sv = __uint_as_float(f[s]) >= lo_f;
+    const uint64_t mk = __ballot(sv);
+    int pos = (int)__builtin_amdgcn_mbcnt_hi(
+        (uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, (uint32_t)n));
+    asm("" : "+v"(pos));  // formed in every lane: the store below needs no branch
+    scr[sv ? min(pos, 255) : 256 + lane] = f[s] | (uint32_t)(s * 64 + lane);
+    n += __popcll(mk);
+  }
+  if (n > 256) return -1;
+  const int k2 = kq - nf;
+  if (n <= 64) return ls_nosa_stage1_finish<1>(scr, n, lo, kq, k2, lo_end, la, lb, n_words, lane);
+  if (n <= 128) return ls_nosa_stage1_finish<2>(scr, n, lo, kq, k2, lo_end, la, lb, n_words, lane);
+  return ls_nosa_stage1_finish<4>(scr, n, lo, kq, k2, lo_end, la, lb, n_words, lane);
+}
+
 // Key widths: stage 1 uses 16-bit keys for 16-bit page scores (KEY32 off);
 // stage 2 uses the top 16 bits of the float32 keys when the CIS page scores
 // are bf16 values (CIS32 off: their low 16 bits are zero), so each bisection
@@ -339,8 +490,18 @@ __device__ __forceinline__ void ls_nosa_topk_row(
     const void* __restrict__ P, int64_t prow, int n_scored, int out_len, int off_bq, int q_idx,
     int init_blocks, int local_blocks, int qk_select, int take, uint32_t pinf1, uint32_t ninf1,
     int lane, int32_t* __restrict__ orow, uint32_t* __restrict__ scr,
-    const int32_t* __restrict__ order, int n_order) {
+    const int32_t* __restrict__ order, int n_order, int bf16) {
   constexpr int NW = (NS + 31) / 32;
+  // Stage 1 ends with the shortlist S as a page bitmap in the wave's scratch
+  // (n_s = |S|); stage 2 then adds the block order's first take - |S| pages
+  // outside S to it.
+  const int n_words = (out_len + 31) >> 5;
+  int n_s = -1;
+  if constexpr (!KEY32 && NS > 4)
+    if (bf16)
+      n_s = ls_nosa_stage1_bf16<NS>((const uint16_t*)P + prow, n_scored, out_len, off_bq,
+                                    init_blocks, local_blocks, qk_select, n_words, lane, scr);
+  if (n_s < 0) {
   // Every +inf (forced or shortlisted) and every -inf is one key, so ties among
   // them go to the lower page as in a stable sort.  Stage 1 keys come from the
   // page-score dtype (pinf1 / ninf1).
@@ -366,11 +527,6 @@ __device__ __forceinline__ void ls_nosa_topk_row(
     else k = ninf1;
     key[s] = k;
   }
-  // Stage 1 ends with the shortlist S as a page bitmap in the wave's scratch
-  // (n_s = |S|); stage 2 then adds the block order's first take - |S| pages
-  // outside S to it.
-  const int n_words = (out_len + 31) >> 5;
-  int n_s = -1;
   if constexpr (!KEY32 && NS > 4) {
     // Long rows: the keys >= lo (lo = the qk_select-th largest of the lanes'
     // two largest keys) are gathered as key << 16 | page in page order, and S
@@ -420,6 +576,7 @@ __device__ __forceinline__ void ls_nosa_topk_row(
       if (lane < 2) scr[2 * s + lane] = lane ? (uint32_t)(m >> 32) : (uint32_t)m;
       n_s += __popcll(m);
     }
+  }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -610,7 +767,8 @@ __global__ __launch_bounds__(256) void ls_nosa_topk_kernel(
     const int32_t* __restrict__ cu_a, const int32_t* __restrict__ blk_off, int batch,
     int64_t total_q, int G, int max_seqlen_q, int out_len, int init_blocks, int local_blocks,
     int qk_select, int take, int block_size, uint32_t pinf1, uint32_t ninf1,
-    const int32_t* __restrict__ order, int64_t n_blk, int n_order, int32_t* __restrict__ topk_idx) {
+    const int32_t* __restrict__ order, int64_t n_blk, int n_order, int bf16,
+    int32_t* __restrict__ topk_idx) {
   __shared__ uint32_t s_scr[4][320];  // per-wave k-th key scratch, then the chosen-page bitmap
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -635,7 +793,7 @@ __global__ __launch_bounds__(256) void ls_nosa_topk_kernel(
   const int n_slots = (out_len + 63) >> 6;
   const int n_ord = n_order < out_len ? n_order : out_len;
 #define LS_ROW(NSV) ls_nosa_topk_row<NSV, KEY32>(P, prow, n_scored, out_len, off_bq, q_idx, \
-    init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, ord, n_ord)
+    init_blocks, local_blocks, qk_select, take, pinf1, ninf1, lane, orow, scr, ord, n_ord, bf16)
   if (n_slots <= 1) return LS_ROW(1);
   if (n_slots <= 2) return LS_ROW(2);
   if (n_slots <= 4 || KPL <= 4) return LS_ROW(KPL < 4 ? KPL : 4);
@@ -657,8 +815,8 @@ static int launch_nosa_topk_k(int out_len, hipStream_t s, const void* P, int64_t
                               const int32_t* cu_q, const int32_t* cu_a, const int32_t* blk_off,
                               int64_t n_blk, int batch, int64_t total_q, int G, int max_q,
                               int init, int local, int qk_select, int take, int bs,
-                              int clip_row, uint32_t pinf1, uint32_t ninf1, int32_t* order,
-                              int32_t* out) {
+                              int clip_row, uint32_t pinf1, uint32_t ninf1, int bf16,
+                              int32_t* order, int32_t* out) {
   const int n_order = take + qk_select;
   const dim3 rgrid((unsigned)n_blk, G, 2);
   const dim3 grid((unsigned)(((int64_t)G * total_q + 3) / 4));
@@ -670,7 +828,7 @@ static int launch_nosa_topk_k(int out_len, hipStream_t s, const void* P, int64_t
     if (int rc = ls_check_launch("ls_nosa_cis_rank_kernel")) return rc;                       \
     hipLaunchKernelGGL((ls_nosa_topk_kernel<K, KEY32>), grid, dim3(256), 0, s, P, ps, cu_q,   \
                        cu_a, blk_off, batch, total_q, G, max_q, out_len, init, local,         \
-                       qk_select, take, bs, pinf1, ninf1, order, n_blk, n_order, out);        \
+                       qk_select, take, bs, pinf1, ninf1, order, n_blk, n_order, bf16, out);  \
   } while (0)
   if (out_len <= 256) LS_NOSA_TOPK(4);
   else if (out_len <= 1024) LS_NOSA_TOPK(16);
@@ -695,7 +853,7 @@ int ls_nosa_topk_launch(int p_dtype, int out_len, const void* P, int64_t p_strid
 #define LS_NOSA_TOPK_ARGS                                                                      \
   out_len, s, P, p_stride, cpg, cpg_g_stride, pg_off, cu_q, cu_a, blk_off, n_blk, batch,     \
       total_q, G, max_seqlen_q, init_blocks, local_blocks, qk_select, take, block_size,       \
-      clip_row, pinf, ninf, order, topk_idx
+      clip_row, pinf, ninf, p_dtype == LS_BF16 ? 1 : 0, order, topk_idx
   if (p_dtype == LS_F32) {
     const uint32_t pinf = ls_order_key32(0x7f800000u), ninf = ls_order_key32(0xff800000u);
     return launch_nosa_topk_k<true>(LS_NOSA_TOPK_ARGS);

@@ -890,19 +890,20 @@ __device__ __forceinline__ int ls_count_nan_keys(const void* __restrict__ P, int
 // keep the slots left after the NaN ones (the lowest forced pages first, as
 // the ties at +inf resolve to the lower page) and the others become -1.
 template <int KPL, bool KEY32>
-__global__ __launch_bounds__(256) void ls_topk_kernel(
+__global__ __launch_bounds__(256, 6) void ls_topk_kernel(
     const void* __restrict__ P, int64_t p_stride, const int32_t* __restrict__ cu_q,
     const int32_t* __restrict__ cu_a, int batch, int64_t total_q, int G, int take,
-    int init_blocks, int local_blocks, int block_size, LsInvalidKeys rule,
+    int init_blocks, int local_blocks, int block_size, LsInvalidKeys rule, int bf16,
     int32_t* __restrict__ topk_idx) {
   __shared__ uint32_t s_scr[4][320];  // per-wave gather space of the k-th key search
   const int lane = threadIdx.x & 63;
   // The wave index is uniform: keep the row and everything derived from it scalar.
+  // (Grid: x = groups of four query rows, y = KV group.)
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t row = (int64_t)blockIdx.x * 4 + wv;
-  if (row >= (int64_t)G * total_q) return;
-  const int g = (int)(row / total_q);
-  const int64_t t = row - (int64_t)g * total_q;
+  const int g = blockIdx.y;
+  const int64_t t = (int64_t)blockIdx.x * 4 + wv;
+  if (t >= total_q) return;
+  const int64_t row = (int64_t)g * total_q + t;
   int32_t* orow = topk_idx + row * take;
   uint32_t* const scr = s_scr[wv];
   const int b = ls_find_segment(cu_q, batch, t);
@@ -923,26 +924,33 @@ __global__ __launch_bounds__(256) void ls_topk_kernel(
   // (Clamped to the row's columns, as the scoring is.)
   const int cn = (int)max((int64_t)0, min((int64_t)(hi_start - lo_end), p_stride - lo_end));
   const int64_t base = row * p_stride + lo_end;
-  for (int i = n_valid + lane; i < take; i += 64) orow[i] = -1;
   if (n_forced >= n_valid) {
     // The budget holds forced pages only: the first n_valid of them in page
     // order, after any NaN-scored other pages (emitted as -1).
     const int n_nan = cn > 0 ? ls_count_nan_keys<KEY32>(P, base, cn, lane, rule) : 0;
     const int n_keep = max(0, n_valid - n_nan);
-    for (int i = lane; i < n_valid; i += 64)
+    for (int i = lane; i < take; i += 64)
       orow[i] = i >= n_keep ? -1 : (i < lo_end ? i : hi_start + (i - lo_end));
     return;
   }
   const int kk = n_valid - n_forced;
 
-  for (int i = lane; i < lo_end; i += 64) orow[i] = i;
+  // One pass over the row's slots: sink pages [0, lo_end), the local pages
+  // [hi_pos, n_valid) and -1 past n_valid; the selection writes the rest.
   const int hi_pos = lo_end + kk;
-  for (int i = lane; i < qp + 1 - hi_start; i += 64) orow[hi_pos + i] = hi_start + i;
+  for (int i = lane; i < take; i += 64) {
+    if (i < lo_end || i >= hi_pos)
+      orow[i] = i < lo_end ? i : (i < n_valid ? hi_start + (i - hi_pos) : -1);
+  }
 
   // Candidates in registers, NS slots of 64; the row's slot count is uniform,
   // so the branch picks one straight-line body per wave.
   auto select = [&]() -> uint32_t {
     if constexpr (!KEY32) {
+      uint32_t T;
+      if (bf16 && ls_topk_select16_bf16<KPL>((const uint16_t*)P + base, cn, kk, lo_end, lane,
+                                               orow, scr, INT32_MAX, rule, T))
+        return T;
       return ls_topk_select16<KPL>(P, base, cn, kk, lo_end, lane, orow, scr, INT32_MAX, rule);
     } else {
       const int n_slots = (cn + 63) >> 6;
@@ -1195,7 +1203,8 @@ void launch_topk_kpl(dim3 grid, hipStream_t s, const void* P, int64_t ps, const 
                      const int32_t* cu_a, int batch, int64_t total_q, int G, int take, int init,
                      int local, int bs, int dt, int32_t* out) {
   hipLaunchKernelGGL((ls_topk_kernel<KPL, KEY32>), grid, dim3(256), 0, s, P, ps, cu_q, cu_a,
-                     batch, total_q, G, take, init, local, bs, prefill_rule(dt), out);
+                     batch, total_q, G, take, init, local, bs, prefill_rule(dt),
+                     dt == LS_BF16 ? 1 : 0, out);
 }
 
 template <bool KEY32>
@@ -1474,7 +1483,7 @@ static int select_prefill_impl(const char* who, const void* q, int64_t q_row_str
                         cu_seqlens_kc, blk, batch, n_blk_launch, init_blocks, local_blocks,
                         block_size, kernel_stride, 0, max_pages, ws + L.p, L.p_stride, G, s)))
     return rc;
-  const dim3 grid((unsigned)(((int64_t)G * total_q + 3) / 4));
+  const dim3 grid((unsigned)((total_q + 3) / 4), G);
   if (dtype == LS_F32)
     return launch_topk<true>(max_pages, grid, s, ws + L.p, L.p_stride, cu_seqlens_q,
                              cu_seqlens_kc, batch, total_q, G, take, init_blocks, local_blocks,

@@ -86,15 +86,18 @@ __device__ __forceinline__ uint32_t ls_topk_row(const void* __restrict__ P, int6
 // bisected from the common bit prefix of lo and the row maximum m1 (per-lane
 // maxima, reduced here), then the chosen columns written in column order.
 // Returns T (uniform).
+// (or_mask is OR-ed into every gathered entry as it is read back: the bf16
+// fast path below gathers raw score bits, which become order keys that way.)
 template <int NP>
 __device__ __forceinline__ uint32_t ls_topk_emit_packed(const uint32_t* __restrict__ scr, int n,
                                                         uint32_t lo, uint32_t m1, int kk,
                                                         int lo_end, int lane,
                                                         int32_t* __restrict__ orow, int id_max,
-                                                        const LsInvalidKeys& rule = LsInvalidKeys()) {
+                                                        const LsInvalidKeys& rule = LsInvalidKeys(),
+                                                        uint32_t or_mask = 0u) {
   uint32_t pk[NP];
 #pragma unroll
-  for (int i = 0; i < NP; ++i) pk[i] = i * 64 + lane < n ? scr[i * 64 + lane] : 0u;
+  for (int i = 0; i < NP; ++i) pk[i] = i * 64 + lane < n ? (scr[i * 64 + lane] | or_mask) : 0u;
   uint32_t hi = m1;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, LS_WAVE));
@@ -268,4 +271,135 @@ __device__ __forceinline__ uint32_t ls_topk_select16(const void* __restrict__ P,
   LS_TOPK16_CASE(96)
 #undef LS_TOPK16_CASE
   return ls_topk_row16<KPL>(P, base, cn, kk, lo_end, lane, orow, scr, id_max, rule);
+}
+
+// Fast path of ls_topk_row16 for a row of bf16 scores whose kk-th largest
+// score is positive and which holds no NaN.  The row is read through a buffer
+// resource bounded at cn columns, so the slots need no address clamping and no
+// per-lane column masks: reads past the row return 0, i.e. +0.0, which only the
+// bound check below has to keep out.  The scores are compared as float32 (the
+// bf16 bits shifted up by 16), which orders them as their order keys do apart
+// from -0 / +0, and that difference cannot matter here:
+//  * the lanes' two largest values (v_maximum / v_med3; a NaN anywhere makes
+//    the lane maximum NaN) are values of distinct row entries or of the +0 read
+//    past the row, and their order keys are at most those entries' keys, so the
+//    kk-th largest of those keys, lo, is a lower bound of the row's kk-th key
+//    when it lies above +0's key (then no +0 read past the row is among the kk);
+//  * every score >= lo (as floats) is gathered with its column (at most 256 of
+//    them), which includes every key >= lo, and none of the +0 past the row;
+//  * all gathered scores are positive, so bf16 | 0x8000 is their order key and
+//    the gathered entries become ls_topk_emit_packed's key << 16 | column with
+//    one OR.
+// Returns false, having written nothing to orow, when a condition fails (kk
+// outside 1..128, a NaN, lo at or below +0, more than 256 gathered); the caller
+// then runs the general path.  Otherwise T is the kk-th largest order key.
+template <int NS>
+__device__ __forceinline__ bool ls_topk_row16_bf16(const uint16_t* __restrict__ row, int cn,
+                                                   int kk, int lo_end, int lane,
+                                                   int32_t* __restrict__ orow,
+                                                   uint32_t* __restrict__ scr, int id_max,
+                                                   const LsInvalidKeys& rule, uint32_t& T) {
+  if (kk < 1 || kk > 128) return false;
+  // One resource bounded at the row's end; each slot's whole byte offset is
+  // a lane register (hidden from the compiler, so that no part of it moves
+  // into the scalar offset, which the hardware range check leaves out).
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)row, (short)0, cn * 2, 0x00020000);
+  uint32_t f[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    uint32_t off = (uint32_t)(lane * 2 + 128 * s);
+    asm("" : "+v"(off));
+    f[s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)off, 0, 0) << 16;
+  }
+  float m1 = -INFINITY, m2 = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const float x = __uint_as_float(f[s]);
+    m2 = __builtin_amdgcn_fmed3f(m1, m2, x);
+    m1 = __builtin_elementwise_maximum(m1, x);
+  }
+  if (__ballot(__builtin_isnan(m1)) != 0ull) return false;
+  const uint32_t k1 = ls_order_key16((uint16_t)(__float_as_uint(m1) >> 16));
+  const uint32_t k2 = ls_order_key16((uint16_t)(__float_as_uint(m2) >> 16));
+  // lo: the kk-th largest of the 128 keys, bisected below the bit prefix that
+  // all of them share (that of the smallest second and the largest first key),
+  // with the loop unrolled.
+  uint32_t kmin = k2, kmax = k1;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, LS_WAVE));
+    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, LS_WAVE));
+  }
+  kmin = (uint32_t)__builtin_amdgcn_readfirstlane((int)kmin);
+  kmax = (uint32_t)__builtin_amdgcn_readfirstlane((int)kmax);
+  const uint32_t dk = kmin ^ kmax;
+  const int top = dk ? 31 - __builtin_clz(dk) : -1;  // highest differing bit
+  uint32_t lo = top >= 0 ? kmin & ~((2u << top) - 1u) : kmin;
+#pragma unroll
+  for (int bit = 15; bit >= 0; --bit) {
+    if (bit <= top) {
+      const uint32_t cand = lo | (1u << bit);
+      const int cnt = __popcll(__ballot(k1 >= cand)) + __popcll(__ballot(k2 >= cand));
+      lo = cnt >= kk ? cand : lo;
+    }
+  }
+  if (lo <= 0x8000u) return false;  // the bound must be a positive score
+  const float lo_f = __uint_as_float((lo & 0x7fffu) << 16);
+  // Gather without branches: a lane whose score is below lo writes a word of
+  // its own past the 256 entries (words 256 + lane), and entries beyond 256
+  // (the row then takes the general path) all land on word 255.
+  int n = 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool sv = __uint_as_float(f[s]) >= lo_f;
+    const uint64_t mk = __ballot(sv);
+    int pos = (int)__builtin_amdgcn_mbcnt_hi(
+        (uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, (uint32_t)n));
+    asm("" : "+v"(pos));  // formed in every lane: the store below needs no branch
+    scr[sv ? min(pos, 255) : 256 + lane] = f[s] | (uint32_t)(s * 64 + lane);
+    n += __popcll(mk);
+  }
+  if (n > 256) return false;
+  if (n <= 64)
+    T = ls_topk_emit_packed<1>(scr, n, lo, k1, kk, lo_end, lane, orow, id_max, rule, 0x80000000u);
+  else if (n <= 128)
+    T = ls_topk_emit_packed<2>(scr, n, lo, k1, kk, lo_end, lane, orow, id_max, rule, 0x80000000u);
+  else
+    T = ls_topk_emit_packed<4>(scr, n, lo, k1, kk, lo_end, lane, orow, id_max, rule, 0x80000000u);
+  return true;
+}
+
+// ls_topk_select16 for bf16 rows of more than four slots through the fast path
+// above (same slot-count steps); false when the row needs the general path
+// (rows of up to four slots always do).
+template <int KPL>
+__device__ __forceinline__ bool ls_topk_select16_bf16(const uint16_t* __restrict__ row, int cn,
+                                                      int kk, int lo_end, int lane,
+                                                      int32_t* __restrict__ orow,
+                                                      uint32_t* __restrict__ scr, int id_max,
+                                                      const LsInvalidKeys& rule, uint32_t& T) {
+  const int n_slots = (cn + 63) >> 6;
+  if (n_slots <= 4 || KPL <= 4) return false;
+#define LS_TOPK16F_CASE(N)                                                                   \
+  if (n_slots <= (N) || KPL <= (N))                                                          \
+    return ls_topk_row16_bf16<(KPL < (N) ? KPL : (N))>(row, cn, kk, lo_end, lane, orow, scr, \
+                                                       id_max, rule, T);
+  LS_TOPK16F_CASE(6)
+  LS_TOPK16F_CASE(8)
+  LS_TOPK16F_CASE(10)
+  LS_TOPK16F_CASE(12)
+  LS_TOPK16F_CASE(14)
+  LS_TOPK16F_CASE(16)
+  LS_TOPK16F_CASE(20)
+  LS_TOPK16F_CASE(24)
+  LS_TOPK16F_CASE(28)
+  LS_TOPK16F_CASE(32)
+  LS_TOPK16F_CASE(40)
+  LS_TOPK16F_CASE(48)
+  LS_TOPK16F_CASE(56)
+  LS_TOPK16F_CASE(64)
+  LS_TOPK16F_CASE(96)
+#undef LS_TOPK16F_CASE
+  return ls_topk_row16_bf16<KPL>(row, cn, kk, lo_end, lane, orow, scr, id_max, rule, T);
 }

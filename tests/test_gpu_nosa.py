@@ -198,6 +198,26 @@ def test_nosa_select_with_nan_and_inf_scores():
     _check_nosa_select(case, cis, rows, topk=24, init=1, local=4, select=6)
 
 
+def test_nosa_select_long_rows_fast_and_general_paths():
+    """Rows of more than 256 pages: bf16 stage 1 takes a fast path while its
+    shortlist bound is a positive score and no score is NaN or +inf, else the
+    general path.  Keys shifted along one direction make most of a row's scores
+    share the sign of q~ . shift (both paths occur), a zero query row ties every
+    page at +0, and a NaN query row scores NaN everywhere."""
+    import dataclasses
+    case = workloads.hidden_space_layer((20000,), hidden=1024, device=DEV, seed=17)
+    gen = torch.Generator(device="cpu").manual_seed(6)
+    shift = (torch.randn(case.k.shape[1:], generator=gen) * 20.0).to(DEV)
+    k = (case.k.float() + shift).to(case.k.dtype)
+    q = case.q.clone()
+    q[[15000, 19999]] = 0
+    q[17000, 3, 5] = float("nan")
+    case = dataclasses.replace(case, q=q, k=k)
+    cis = _cis(20000, 2, seed=17)
+    rows = sorted(set(spread_rows(case.cu_host, per_seq=64)) | {15000, 17000, 19999})
+    _check_nosa_select(case, cis, rows, topk=96, init=1, local=16, select=24)
+
+
 def test_nosa_select_fp32_and_fp16():
     case = workloads.head_space_layer(5000, device=DEV, seed=13)
     cis = _cis(5000, 2, torch.float32, seed=13)

@@ -1,6 +1,8 @@
 """GPU parity of page selection and block-sparse attention against the oracle,
 on the benchmark's synthetic workloads (small sizes in full, 32K on sampled rows
 plus size-independent plan invariants)."""
+import dataclasses
+
 import pytest
 import torch
 
@@ -96,6 +98,44 @@ def test_batch_without_any_compressed_key():
         cu_seqlens_host=case.cu_host, return_topk_idx=True)
     torch.cuda.synchronize()
     assert torch.equal(ids2, ids) and not bool(out.any())
+
+
+def test_select_rows_with_nonpositive_kth_scores():
+    """bf16 rows take a fast top-k path only while their kk-th score is positive
+    (reads past the row come back as +0); rows whose kk-th score is zero or
+    negative take the general path.  The keys are shifted along one direction,
+    so most of a row's scores share the sign of q~ . shift, and some query rows
+    are zero (every score +0, all tied).  Long rows of both kinds must match the
+    oracle."""
+    case = workloads.hidden_space_layer((32768,), hidden=1024, device=DEV, seed=41)
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    shift = (torch.randn(case.k.shape[1:], generator=gen) * 20.0).to(DEV)
+    k = (case.k.float() + shift).to(case.k.dtype)
+    q = case.q.clone()
+    zero_rows = [20000, 20001, 31000]
+    q[zero_rows] = 0
+    case = dataclasses.replace(case, q=q, k=k)
+    rows = sorted(set(spread_rows(case.cu_host, per_seq=96)) | set(zero_rows))
+    kc, cu_c, ids = _select(case)
+    want, scores = oracle_select_rows(case, kc.cpu(), cu_c.cpu().tolist(), rows, case.q.dtype)
+    rep = oracle.check_topk(ids.cpu()[:, rows], want, scores, case.q.dtype)
+    print(f"\nselect parity (shifted keys): {rep}")
+    assert rep.ok, str(rep)
+    take = ids.shape[-1]
+    pos = nonpos = 0
+    for g in range(scores.shape[0]):
+        for i in range(len(rows)):
+            s = scores[g, i]
+            fin = s[torch.isfinite(s)]
+            n_forced = int(torch.isposinf(s).sum())
+            kk = min(take, n_forced + fin.numel()) - n_forced
+            if fin.numel() <= 256 or kk < 1:
+                continue  # rows of up to four slots always take the general path
+            kth = float(fin.sort(descending=True).values[kk - 1])
+            pos += kth > 0
+            nonpos += kth <= 0
+    print(f"long rows with a positive kk-th score: {pos}, zero or negative: {nonpos}")
+    assert pos >= 10 and nonpos >= 10
 
 
 def test_select_32k_sampled_rows():
