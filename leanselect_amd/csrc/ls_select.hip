@@ -889,6 +889,9 @@ __device__ __forceinline__ int ls_count_nan_keys(const void* __restrict__ P, int
 // only when there are more of them than kk, in which case the forced pages
 // keep the slots left after the NaN ones (the lowest forced pages first, as
 // the ties at +inf resolve to the lower page) and the others become -1.
+// With bf16 set (bf16 page scores) long rows try ls_topk_select16_bf16 first.
+// At least six waves per SIMD: the rows' latency chains (row setup, loads,
+// stores) overlap across waves.
 template <int KPL, bool KEY32>
 __global__ __launch_bounds__(256, 6) void ls_topk_kernel(
     const void* __restrict__ P, int64_t p_stride, const int32_t* __restrict__ cu_q,
