@@ -218,6 +218,18 @@ def test_nosa_select_long_rows_fast_and_general_paths():
     _check_nosa_select(case, cis, rows, topk=96, init=1, local=16, select=24)
 
 
+def test_nosa_select_long_rows_of_tied_scores():
+    """Every key row equal: every page of a row ties in stage 1, so rows with a
+    positive score gather more than 256 ties and leave the fast path, and the
+    shortlist takes the lowest pages."""
+    import dataclasses
+    case = workloads.hidden_space_layer((20000,), hidden=1024, device=DEV, seed=18)
+    case = dataclasses.replace(case, k=case.k[:1].expand_as(case.k).contiguous())
+    cis = _cis(20000, 2, seed=18)
+    rows = spread_rows(case.cu_host, per_seq=48)
+    _check_nosa_select(case, cis, rows, topk=96, init=1, local=16, select=24)
+
+
 def test_nosa_select_fp32_and_fp16():
     case = workloads.head_space_layer(5000, device=DEV, seed=13)
     cis = _cis(5000, 2, torch.float32, seed=13)

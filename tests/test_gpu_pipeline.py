@@ -138,6 +138,24 @@ def test_select_rows_with_nonpositive_kth_scores():
     assert pos >= 10 and nonpos >= 10
 
 
+def test_select_rows_of_tied_scores():
+    """Every key row equal, so every page of a row scores the same: rows whose
+    score is positive pass the fast path's bound but gather more than 256 ties
+    (the general path takes over), the others fail the bound.  Ties go to the
+    lowest pages."""
+    case = workloads.hidden_space_layer((24576,), hidden=1024, device=DEV, seed=43)
+    k = case.k[:1].expand_as(case.k).contiguous()
+    case = dataclasses.replace(case, k=k)
+    rows = spread_rows(case.cu_host, per_seq=96)
+    _, _, ids, rep = _check_select(case, rows=rows)
+    assert rep.exact_rows == rep.rows
+    # The chosen non-forced pages are the lowest ones: 1, 2, ... (sink page 0).
+    for r in rows:
+        qp = r // 64
+        if qp > case.topk:
+            assert ids[0, r, : case.topk - 5].tolist() == list(range(case.topk - 5))
+
+
 def test_select_32k_sampled_rows():
     case = workloads.hidden_space_layer((32768,), device=DEV, seed=3)
     rows = spread_rows(case.cu_host, per_seq=128)
