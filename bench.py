@@ -86,11 +86,19 @@ def attention_keys(ids: torch.Tensor, cu_host: list[int]) -> int:
     return int((keys * valid).sum())
 
 
-def plan_locality(ids: torch.Tensor, cu_host: list[int], tile: int = 16) -> dict:
+def attention_tile_rows(take: int) -> int:
+    """Query rows per block of the sparse-attention kernel: 24 while a row holds at
+    most 85 ids (a tile's page union then fits the 2048-entry union table), else 16."""
+    return 24 if take <= 2048 // 24 else 16
+
+
+def plan_locality(ids: torch.Tensor, cu_host: list[int], tile: int | None = None) -> dict:
     """Mean distinct pages of a ``tile``-row query tile's plans (per KV group), and
     the mean number of the tile's rows that chose each of those pages: how much
-    K/V one staged page serves."""
+    K/V one staged page serves. ``tile`` defaults to the attention kernel's."""
     G, N, T = ids.shape
+    if tile is None:
+        tile = attention_tile_rows(T)
     unions, chosen = 0.0, 0.0
     n_tiles = 0
     for b in range(len(cu_host) - 1):

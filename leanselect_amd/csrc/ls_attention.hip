@@ -6,7 +6,7 @@
 // keys are those of the valid ids in topk_idx[g, t, :] (each page once) with
 // j <= t + len_k - len_q when causal; all H/G heads of the group share the plan.
 //
-// Design (one workgroup per 16 query rows of one KV group and 16-head tile):
+// Design (one workgroup per 16 or 24 query rows of one KV group and 16-head tile):
 //   * the plan row is turned into an ascending, duplicate-free page list with
 //     an LDS bitmap (ids past the causal frontier are dropped);
 //   * S^T = K . Q^T on v_mfma_f32_16x16x32: keys are MFMA rows, the 16 heads of
@@ -87,22 +87,21 @@ __global__ void ls_attn_status_clear_kernel(int32_t* __restrict__ status) {
 }
 
 // ---------------------------------------------------------------------------
-// Tile kernel: one workgroup = LS_ATT_TILE (16) consecutive query rows of one
-// sequence and one KV group for 16 of its query heads (8 waves x 2 rows, two
-// waves per SIMD).  The rows' page plans are OR-ed into a union page list;
+// Tile kernel: one workgroup = 8 x TPW consecutive query rows of one sequence
+// and one KV group for 16 of its query heads (8 waves x TPW rows, two waves per
+// SIMD; TPW = 3, 24-row tiles, when a row has at most LS_ATT_UNION_CAP / 24
+// ids, else TPW = 2).  The rows' page plans are OR-ed into a union page list;
 // each union page of staged K and V^T is streamed once into a 4-stage LDS ring
 // with direct global->LDS loads, and every row that selected the page runs its
 // MFMAs on it.  Rows that did not select a page skip it (no masked-out work).
-// A wave keeps its two rows' O^T accumulators (2 x 8 x 4 floats per lane) and
-// Q^T fragments in registers.
+// A wave keeps its rows' O^T accumulators (TPW x 8 x 4 floats per lane) and
+// Q^T fragments in registers.  Larger tiles share each page copy among more
+// rows; three rows of O and Q are what the register file holds at two waves per
+// SIMD (with the V^T fragments read per row instead of shared).
 // ---------------------------------------------------------------------------
-#ifndef LS_ATT_TPW
-#define LS_ATT_TPW 2                         // rows per wave
-#endif
 #ifndef LS_ATT_WAVES
 #define LS_ATT_WAVES 8                       // waves per workgroup
 #endif
-#define LS_ATT_TILE (LS_ATT_WAVES * LS_ATT_TPW)  // rows per workgroup (<= 32)
 #define LS_ATT_THREADS (64 * LS_ATT_WAVES)
 #define LS_ATT_STAGES 4
 #define LS_ATT_KBYTES (64 * 256)             // K page: 64 rows x 256 B
@@ -117,7 +116,18 @@ __global__ void ls_attn_status_clear_kernel(int32_t* __restrict__ status) {
 #ifndef LS_ATT_SPIN_SLEEP
 #define LS_ATT_SPIN_SLEEP 1                  // s_sleep units between a waiting wave's polls
 #endif
-#define LS_ATT_MAX_UNION (LS_ATT_TILE * LS_ATTN_MAX_TAKE)
+#define LS_ATT_UNION_CAP (64 * 32)           // union pages of a tile: one 32-bit need word per lane
+
+// Tile geometry for TPW rows per wave: rows per tile, the most ids per row it
+// accepts (so that its union fits LS_ATT_UNION_CAP) and the union bound.
+template <int TPW>
+struct LsAttTile {
+  static constexpr int kTile = LS_ATT_WAVES * TPW;
+  static constexpr int kMaxTake = TPW == 2 ? LS_ATTN_MAX_TAKE : LS_ATT_UNION_CAP / kTile;
+  static constexpr int kMaxUnion = kTile * kMaxTake;
+  static_assert(kTile <= 32, "row masks are 32-bit");
+  static_assert(kMaxUnion <= LS_ATT_UNION_CAP, "one need word per lane");
+};
 
 typedef _Float16 ls_half2 __attribute__((ext_vector_type(2)));
 typedef float ls_float2 __attribute__((ext_vector_type(2)));
@@ -222,7 +232,7 @@ __device__ __forceinline__ float ls_sum_f16x2(uint32_t x, float acc) {
 // BIAS adds a per-key score bias (the NOSA eviction score, pre-scaled to base
 // 2): weight_j = 2^(scale_log2 * q.k_j + cb_j).  cb[g][64 pg_off[b] + j] is
 // staged like V^T and copied with each page (256 B per stage).
-template <int DT, bool BIAS>
+template <int DT, bool BIAS, int TPW>
 __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_tile_kernel(
     const uint16_t* __restrict__ qg, int64_t q_rs, const uint8_t* __restrict__ kv, int64_t lpad,
     const int32_t* __restrict__ vexp, const float* __restrict__ cb,
@@ -233,15 +243,18 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     float scale_log2, int causal, uint16_t* __restrict__ out, float* __restrict__ lse,
     int per_xcd, int32_t* __restrict__ status, int spin_limit) {
   constexpr int D = 128;
-  constexpr uint32_t ROWS_MASK = LS_ATT_TPW == 32 ? 0xffffffffu : ((1u << LS_ATT_TPW) - 1u);
+  constexpr int TILE = LsAttTile<TPW>::kTile;
+  constexpr int MAX_UNION = LsAttTile<TPW>::kMaxUnion;
+  constexpr uint32_t ROWS_MASK = (1u << TPW) - 1u;
   // The per-row page bitmaps are only needed before streaming starts and
   // share their LDS with the ring.
   __shared__ __align__(16) uint8_t s_ring[LS_ATT_STAGES * LS_ATT_STAGE_BYTES];
-  // Union entry: page << 16 | mask of the tile rows that selected it.
-  __shared__ uint32_t s_umeta[LS_ATT_MAX_UNION];
-  __shared__ uint8_t s_uneed[LS_ATT_MAX_UNION];  // waves with a row on the page
+  // Union entry: the mask of the tile rows that selected the page, and the page.
+  __shared__ uint32_t s_umeta[MAX_UNION];
+  __shared__ uint16_t s_upage[MAX_UNION];
+  __shared__ uint8_t s_uneed[MAX_UNION];  // waves with a row on the page
   // Bit u of s_wneed[w] is set when a row of wave w selected union page u.
-  __shared__ uint32_t s_wneed[LS_ATT_WAVES][LS_ATT_MAX_UNION / 32];
+  __shared__ uint32_t s_wneed[LS_ATT_WAVES][MAX_UNION / 32];
   __shared__ int s_wsum[LS_ATT_WAVES];
   // Ring protocol: s_next = next union page to be claimed for copying;
   // s_rdy[st][0] = union index + 1 of the page whose copy into stage st has
@@ -250,12 +263,12 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   __shared__ uint32_t s_next, s_done[LS_ATT_STAGES];
   __shared__ __align__(8) uint32_t s_rdy[LS_ATT_STAGES][2];
   __shared__ __align__(16) float s_bias[BIAS ? LS_ATT_STAGES * 64 : 4];
-  static_assert(LS_ATT_TILE * LS_ATT_WORDS * 4 <= LS_ATT_STAGES * LS_ATT_STAGE_BYTES,
+  static_assert(TILE * LS_ATT_WORDS * 4 <= LS_ATT_STAGES * LS_ATT_STAGE_BYTES,
                 "page bitmaps must fit in the ring");
-  static_assert(LS_ATT_TILE <= 32, "row masks are 32-bit");
+  static_assert(TILE <= 32, "row masks are 32-bit");
   static_assert(LS_ATT_WORDS <= LS_ATT_THREADS, "one bitmap word per thread");
 #ifdef LS_ATT_NO_ALIAS
-  __shared__ uint32_t s_bits[LS_ATT_TILE][LS_ATT_WORDS];
+  __shared__ uint32_t s_bits[TILE][LS_ATT_WORDS];
 #else
   uint32_t(*s_bits)[LS_ATT_WORDS] = reinterpret_cast<uint32_t(*)[LS_ATT_WORDS]>(s_ring);
 #endif
@@ -282,8 +295,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   const bool head_ok = head < gs;
 
   const int b = ls_find_segment(tile_off, batch, tile);
-  const int64_t t0 = (int64_t)cu_q[b] + LS_ATT_TILE * (tile - tile_off[b]);
-  const int n_rows = (int)min((int64_t)LS_ATT_TILE, (int64_t)cu_q[b + 1] - t0);
+  const int64_t t0 = (int64_t)cu_q[b] + TILE * (tile - tile_off[b]);
+  const int n_rows = (int)min((int64_t)TILE, (int64_t)cu_q[b + 1] - t0);
   const int lq = cu_q[b + 1] - cu_q[b];
   const int lk = cu_k[b + 1] - cu_k[b];
   const int64_t vbase = 64LL * pg_off[b];
@@ -301,15 +314,15 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
 
   // ---- per-row state: Q^T fragments (B operand), softmax stats, O^T ----
   // (the Q loads are issued first; they land while the page list is built)
-  ls_u32x4 qf[LS_ATT_TPW][4];
+  ls_u32x4 qf[TPW][4];
   // m_run: running max in scaled base-2 units (score * scale_log2); thr: the
   // raw score above which a key would exceed m_run by more than 2^8.
-  float m_run[LS_ATT_TPW], l_run[LS_ATT_TPW], thr[LS_ATT_TPW];
-  int jmax_r[LS_ATT_TPW];
-  ls_f32x4 o[LS_ATT_TPW][8];
+  float m_run[TPW], l_run[TPW], thr[TPW];
+  int jmax_r[TPW];
+  ls_f32x4 o[TPW][8];
 #pragma unroll
-  for (int j = 0; j < LS_ATT_TPW; ++j) {
-    const int row = w * LS_ATT_TPW + j;
+  for (int j = 0; j < TPW; ++j) {
+    const int row = w * TPW + j;
     const int64_t t = t0 + min(row, n_rows - 1);
     const uint16_t* qrow = qg + t * q_rs + ((int64_t)g * gs + (head_ok ? head : 0)) * D + 8 * q;
 #pragma unroll
@@ -325,9 +338,9 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     for (int db = 0; db < 8; ++db) o[j][db] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
   }
   // ---- per-row page bitmaps and their sorted union ----
-  for (int i = tid; i < LS_ATT_TILE * nwords; i += LS_ATT_THREADS) s_bits[i / nwords][i % nwords] = 0u;
-  for (int i = tid; i < LS_ATT_WAVES * (LS_ATT_MAX_UNION / 32); i += LS_ATT_THREADS)
-    s_wneed[i / (LS_ATT_MAX_UNION / 32)][i % (LS_ATT_MAX_UNION / 32)] = 0u;
+  for (int i = tid; i < TILE * nwords; i += LS_ATT_THREADS) s_bits[i / nwords][i % nwords] = 0u;
+  for (int i = tid; i < LS_ATT_WAVES * (MAX_UNION / 32); i += LS_ATT_THREADS)
+    s_wneed[i / (MAX_UNION / 32)][i % (MAX_UNION / 32)] = 0u;
   if (tid < LS_ATT_STAGES) {
     s_rdy[tid][0] = 0u;
     s_done[tid] = 0u;
@@ -345,9 +358,9 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     }
   }
   __syncthreads();
-  uint32_t word = 0u, row_word[LS_ATT_TILE];
+  uint32_t word = 0u, row_word[TILE];
 #pragma unroll
-  for (int i = 0; i < LS_ATT_TILE; ++i) {
+  for (int i = 0; i < TILE; ++i) {
     row_word[i] = tid < nwords ? s_bits[i][tid] : 0u;
     word |= row_word[i];
   }
@@ -394,17 +407,18 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     const int page = tid * 32 + bit;
     uint32_t rows = 0u;
 #pragma unroll
-    for (int i = 0; i < LS_ATT_TILE; ++i) rows |= ((row_word[i] >> bit) & 1u) << i;
+    for (int i = 0; i < TILE; ++i) rows |= ((row_word[i] >> bit) & 1u) << i;
     const int dst = (int)(((uint32_t)pos * (uint32_t)stride) % (uint32_t)n_union);
     int n_waves = 0;
 #pragma unroll
     for (int i = 0; i < LS_ATT_WAVES; ++i) {
-      if (((rows >> (LS_ATT_TPW * i)) & ROWS_MASK) != 0u) {
+      if (((rows >> (TPW * i)) & ROWS_MASK) != 0u) {
         ++n_waves;
         atomicOr(&s_wneed[i][dst >> 5], 1u << (dst & 31));
       }
     }
-    s_umeta[dst] = ((uint32_t)page << 16) | rows;
+    s_umeta[dst] = rows;
+    s_upage[dst] = (uint16_t)page;
     s_uneed[dst] = (uint8_t)n_waves;
     ++pos;
   }
@@ -414,8 +428,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   LS_WAIT_VMCNT(0);
   // This wave's pages: bit b of lane l is set when one of its rows selected
   // union page 32 l + b (the union holds at most 64 x 32 pages).
-  static_assert(LS_ATT_MAX_UNION <= 64 * 32, "one need word per lane");
-  const uint32_t wneed = lane < LS_ATT_MAX_UNION / 32 ? s_wneed[w][lane] : 0u;
+  static_assert(MAX_UNION <= 64 * 32, "one need word per lane");
+  const uint32_t wneed = lane < MAX_UNION / 32 ? s_wneed[w][lane] : 0u;
 
   // ---- staging ----
   // One wave copies a whole union page into its stage: the page's staged
@@ -441,7 +455,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   const uint32_t ring_off = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(ls_lds_void*)s_ring);
   auto issue_page = [&](int ui_copy) {
-    const int page = __builtin_amdgcn_readfirstlane((int)(s_umeta[ui_copy] >> 16));
+    const int page = __builtin_amdgcn_readfirstlane((int)s_upage[ui_copy]);
     const uint32_t kb = ring_off + (ui_copy % LS_ATT_STAGES) * LS_ATT_STAGE_BYTES;
     // The staged page is the stage's byte image: 32 contiguous 1 KB copies.
     const uint8_t* src = kvgrp + (int64_t)page * LS_ATT_STAGE_BYTES;
@@ -511,7 +525,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       const int base = 64 * page + 32 * c;
       uint32_t need = 0;
 #pragma unroll
-      for (int j = 0; j < LS_ATT_TPW; ++j) need |= (uint32_t)(((sel >> j) & 1u) && base <= jmax_r[j]) << j;
+      for (int j = 0; j < TPW; ++j) need |= (uint32_t)(((sel >> j) & 1u) && base <= jmax_r[j]) << j;
       need = __builtin_amdgcn_readfirstlane(need);
       if (!need) continue;
       // The chunk's K and V^T fragments are read once and shared by the rows.
@@ -525,7 +539,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       }
       // V^T row 16 db + r (so (row >> 1) & 7 == (r >> 1) & 7), logical chunk 4c + q.
       const uint8_t* vrow = vb + r * 128 + (((4 * c + q) ^ ((r >> 1) & 7)) << 4);
-      if constexpr (LS_ATT_TPW > 1) {
+      if constexpr (TPW == 2) {  // two rows share the chunk's V^T fragments
 #pragma unroll
         for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
       }
@@ -597,7 +611,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
         }
         const float lsum = ls_sum_f16x2(pf[3], ls_sum_f16x2(pf[2], ls_sum_f16x2(pf[1], ls_sum_f16x2(pf[0], 0.f))));
         l_run[j] = fmaf(lsum, p_unscale, l_run[j]);
-        if constexpr (LS_ATT_TPW == 1) {  // one row: V^T fragments are read where they are used
+        if constexpr (TPW != 2) {  // V^T fragments are read where they are used
 #pragma unroll
           for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
         }
@@ -605,7 +619,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
         for (int db = 0; db < 8; ++db) o[j][db] = LsElem<LS_F16>::mfma(vf[db], pf, o[j][db]);
       };
 #pragma unroll
-      for (int j = 0; j < LS_ATT_TPW; ++j) {
+      for (int j = 0; j < TPW; ++j) {
         if (!((need >> j) & 1u)) continue;
         ls_f32x4 s0, s1;
         qk(j, s0, s1);
@@ -626,6 +640,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   // The next page's union entry is read before the current page is computed.
   int ui = next_page(-1);
   uint32_t meta = ui < n_union ? s_umeta[ui] : 0u;
+  int page_cur = ui < n_union ? (int)s_upage[ui] : 0;
   while (ui < n_union) {
     uint64_t sw = stage_word(ui);
     if (!is_ready(ui, sw)) {
@@ -649,8 +664,9 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
 
     const int nxt = next_page(ui);
     const uint32_t meta_next = nxt < n_union ? s_umeta[nxt] : 0u;
+    const int page_next = nxt < n_union ? (int)s_upage[nxt] : 0;
     const uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)meta);
-    compute_page(ui, (int)(m >> 16), (m >> (LS_ATT_TPW * w)) & ROWS_MASK,
+    compute_page(ui, __builtin_amdgcn_readfirstlane(page_cur), (m >> (TPW * w)) & ROWS_MASK,
                  __builtin_amdgcn_readfirstlane((int)(uint32_t)(sw >> 32)));
     // Done with the stage (the release orders this wave's reads of it first).
     if (lane == 0)
@@ -658,6 +674,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
                              __HIP_MEMORY_SCOPE_WORKGROUP);
     ui = nxt;
     meta = meta_next;
+    page_cur = page_next;
   }
   LS_WAIT_VMCNT(0);  // no copy of this wave may land after the workgroup ends
 
@@ -669,8 +686,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
                             status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) &
                         LS_ATTN_RING_TIMEOUT) != 0;
 #pragma unroll
-  for (int j = 0; j < LS_ATT_TPW; ++j) {
-    const int row = w * LS_ATT_TPW + j;
+  for (int j = 0; j < TPW; ++j) {
+    const int row = w * TPW + j;
     float l_tot = l_run[j] + ls_shfl_xor(l_run[j], 16);
     l_tot += ls_shfl_xor(l_tot, 32);
     if (row >= n_rows || !head_ok) continue;
@@ -738,12 +755,12 @@ AttnWs attn_ws(int64_t total_k, int batch, int G, bool bias) {
   L.tiles = off; off += ls_align256((size_t)(batch + 1) * 4);
   L.vexp = off; off += ls_align256((size_t)G * L.n_pages * 4);
   L.cb = off; off += bias ? ls_align256((size_t)G * L.lpad * 4) : 0;
-  L.tok = off; off += ls_align256((size_t)(LS_ATT_MAX_UNION + 1) * 4);
+  L.tok = off; off += ls_align256((size_t)(LS_ATT_UNION_CAP + 1) * 4);
   L.total = off;
   return L;
 }
 
-template <int DT, bool BIAS>
+template <int DT, bool BIAS, int TPW>
 void launch_tile(dim3 grid, hipStream_t s, const void* q, int64_t q_rs, const uint8_t* kv,
                  const AttnWs& L, const int32_t* vexp, const float* cb,
                  const int32_t* tok,
@@ -751,7 +768,7 @@ void launch_tile(dim3 grid, hipStream_t s, const void* q, int64_t q_rs, const ui
                  const int32_t* tiles, int batch, int64_t total_q, int G, int gs,
                  const int32_t* topk_idx, int take, float scale_log2, int causal, void* out,
                  float* lse, int32_t* status) {
-  hipLaunchKernelGGL((ls_attn_tile_kernel<DT, BIAS>), grid, dim3(LS_ATT_THREADS), 0, s,
+  hipLaunchKernelGGL((ls_attn_tile_kernel<DT, BIAS, TPW>), grid, dim3(LS_ATT_THREADS), 0, s,
                      (const uint16_t*)q, q_rs, kv, L.lpad, vexp, cb, tok,
                      L.n_pages, cu_q, cu_k, pg, tiles, batch, total_q, G, gs, topk_idx, take,
                      scale_log2, causal, (uint16_t*)out, lse, (int)(grid.x / 8), status,
@@ -803,8 +820,11 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   float* cb = bias ? (float*)(ws + L.cb) : nullptr;
   int32_t* tok = (int32_t*)(ws + L.tok);
   int32_t* status = status_out ? status_out : (int32_t*)(ws + L.status);
+  // 24-row tiles when every row's ids fit their union bound, else 16-row tiles.
+  const bool tile24 = take <= LsAttTile<3>::kMaxTake;
+  const int tile_rows = tile24 ? LsAttTile<3>::kTile : LsAttTile<2>::kTile;
   hipLaunchKernelGGL(ls_attn_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens_q, cu_seqlens_k,
-                     batch, LS_ATT_TILE, pg, tiles, tok, LS_ATT_MAX_UNION + 1, status);
+                     batch, tile_rows, pg, tiles, tok, LS_ATT_UNION_CAP + 1, status);
   int rc = ls_check_launch("ls_attn_plan_kernel");
   if (rc) return rc;
   if (total_k > 0) {
@@ -834,7 +854,7 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   const int gs = num_heads / num_kv_heads;
   const float scale = softmax_scale > 0.f ? softmax_scale : 1.0f / sqrtf((float)head_dim);
   const float scale_log2 = scale * 1.4426950408889634f;
-  const int64_t tile_bound = (total_q + LS_ATT_TILE - 1) / LS_ATT_TILE + batch;
+  const int64_t tile_bound = (total_q + tile_rows - 1) / tile_rows + batch;
   constexpr int64_t kRound = 8 * LS_ATT_XCD_CHUNK;  // whole runs on every XCD
   const dim3 grid((unsigned)(kRound * ((tile_bound + kRound - 1) / kRound)), num_kv_heads,
                   (gs + 15) / 16);
@@ -842,12 +862,22 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   grid, s, q, q_row_stride, kv, L, vexp, cb, tok, cu_seqlens_q, cu_seqlens_k, pg,              \
       tiles, batch, total_q, num_kv_heads, gs, topk_idx, take, scale_log2, causal, out, lse, \
       status
-  if (dtype == LS_BF16) {
-    if (bias) launch_tile<LS_BF16, true>(LS_TILE_ARGS);
-    else launch_tile<LS_BF16, false>(LS_TILE_ARGS);
+  if (tile24) {
+    if (dtype == LS_BF16) {
+      if (bias) launch_tile<LS_BF16, true, 3>(LS_TILE_ARGS);
+      else launch_tile<LS_BF16, false, 3>(LS_TILE_ARGS);
+    } else {
+      if (bias) launch_tile<LS_F16, true, 3>(LS_TILE_ARGS);
+      else launch_tile<LS_F16, false, 3>(LS_TILE_ARGS);
+    }
   } else {
-    if (bias) launch_tile<LS_F16, true>(LS_TILE_ARGS);
-    else launch_tile<LS_F16, false>(LS_TILE_ARGS);
+    if (dtype == LS_BF16) {
+      if (bias) launch_tile<LS_BF16, true, 2>(LS_TILE_ARGS);
+      else launch_tile<LS_BF16, false, 2>(LS_TILE_ARGS);
+    } else {
+      if (bias) launch_tile<LS_F16, true, 2>(LS_TILE_ARGS);
+      else launch_tile<LS_F16, false, 2>(LS_TILE_ARGS);
+    }
   }
 #undef LS_TILE_ARGS
   return ls_check_launch("ls_attn_tile_kernel");
