@@ -45,6 +45,7 @@ sys.path.insert(0, str(ROOT))
 from leanselect_amd import workloads  # noqa: E402
 from leanselect_amd.ops import (compress_k, leanselect_prefill_topk_idx,  # noqa: E402
                                 nosa_prefill_topk_idx, nosa_sparse_attention, sparse_attention)
+from leanselect_amd.ops.attention import attention_tile_rows  # noqa: E402
 
 WORKLOADS = {
     "minicpm41_8b_layer_128k": dict(seq_lens=(131072,)),
@@ -84,12 +85,6 @@ def attention_keys(ids: torch.Tensor, cu_host: list[int]) -> int:
     valid = p >= 0
     keys = torch.clamp(jmax[None, :, None] - 64 * p + 1, min=0, max=64)
     return int((keys * valid).sum())
-
-
-def attention_tile_rows(take: int) -> int:
-    """Query rows per block of the sparse-attention kernel: 24 while a row holds at
-    most 85 ids (a tile's page union then fits the 2048-entry union table), else 16."""
-    return 24 if take <= 2048 // 24 else 16
 
 
 def plan_locality(ids: torch.Tensor, cu_host: list[int], tile: int | None = None) -> dict:

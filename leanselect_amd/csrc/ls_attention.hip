@@ -245,6 +245,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   constexpr int D = 128;
   constexpr int TILE = LsAttTile<TPW>::kTile;
   constexpr int MAX_UNION = LsAttTile<TPW>::kMaxUnion;
+  constexpr int NEED_WORDS = (MAX_UNION + 31) / 32;  // need-mask words per wave
   constexpr uint32_t ROWS_MASK = (1u << TPW) - 1u;
   // The per-row page bitmaps are only needed before streaming starts and
   // share their LDS with the ring.
@@ -254,7 +255,7 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   __shared__ uint16_t s_upage[MAX_UNION];
   __shared__ uint8_t s_uneed[MAX_UNION];  // waves with a row on the page
   // Bit u of s_wneed[w] is set when a row of wave w selected union page u.
-  __shared__ uint32_t s_wneed[LS_ATT_WAVES][MAX_UNION / 32];
+  __shared__ uint32_t s_wneed[LS_ATT_WAVES][NEED_WORDS];
   __shared__ int s_wsum[LS_ATT_WAVES];
   // Ring protocol: s_next = next union page to be claimed for copying;
   // s_rdy[st][0] = union index + 1 of the page whose copy into stage st has
@@ -339,8 +340,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   }
   // ---- per-row page bitmaps and their sorted union ----
   for (int i = tid; i < TILE * nwords; i += LS_ATT_THREADS) s_bits[i / nwords][i % nwords] = 0u;
-  for (int i = tid; i < LS_ATT_WAVES * (MAX_UNION / 32); i += LS_ATT_THREADS)
-    s_wneed[i / (MAX_UNION / 32)][i % (MAX_UNION / 32)] = 0u;
+  for (int i = tid; i < LS_ATT_WAVES * NEED_WORDS; i += LS_ATT_THREADS)
+    s_wneed[i / NEED_WORDS][i % NEED_WORDS] = 0u;
   if (tid < LS_ATT_STAGES) {
     s_rdy[tid][0] = 0u;
     s_done[tid] = 0u;
@@ -428,8 +429,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   LS_WAIT_VMCNT(0);
   // This wave's pages: bit b of lane l is set when one of its rows selected
   // union page 32 l + b (the union holds at most 64 x 32 pages).
-  static_assert(MAX_UNION <= 64 * 32, "one need word per lane");
-  const uint32_t wneed = lane < MAX_UNION / 32 ? s_wneed[w][lane] : 0u;
+  static_assert(NEED_WORDS <= 64, "one need word per lane");
+  const uint32_t wneed = lane < NEED_WORDS ? s_wneed[w][lane] : 0u;
 
   // ---- staging ----
   // One wave copies a whole union page into its stage: the page's staged
@@ -641,15 +642,18 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   int ui = next_page(-1);
   uint32_t meta = ui < n_union ? s_umeta[ui] : 0u;
   int page_cur = ui < n_union ? (int)s_upage[ui] : 0;
+  int spins = spin_limit;  // bound of this wave's next wait (in polls)
   while (ui < n_union) {
     uint64_t sw = stage_word(ui);
     if (!is_ready(ui, sw)) {
       // Bounded wait (the protocol cannot deadlock; the bound only guarantees
       // that a wave always finishes).  A wave whose wait expires reports it
-      // in the status word and goes on; the host turns the status into an
-      // error, and the epilogue below writes NaN rows once it is set.
+      // in the status word and goes on without waiting again (its outputs are
+      // void), so a broken ring costs one bound per wave, not one per page;
+      // the host turns the status into an error, and the epilogue below
+      // writes NaN rows once it is set.
       bool landed = false;
-      for (int spin = 0; spin < spin_limit; ++spin) {
+      for (int spin = 0; spin < spins; ++spin) {
         if (!try_claim(ui)) __builtin_amdgcn_s_sleep(LS_ATT_SPIN_SLEEP);
         sw = stage_word(ui);
         if (is_ready(ui, sw)) {
@@ -657,9 +661,12 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
           break;
         }
       }
-      if (!landed && lane == 0)
-        __hip_atomic_fetch_or(status, LS_ATTN_RING_TIMEOUT, __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
+      if (!landed) {
+        spins = 0;
+        if (lane == 0)
+          __hip_atomic_fetch_or(status, LS_ATTN_RING_TIMEOUT, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
 
     const int nxt = next_page(ui);

@@ -1,7 +1,7 @@
 """GPU parity at the benchmark configurations' full sizes, on sampled rows:
 
 * the 128K MiniCPM4.1-8B attention layer (selection and attention, including
-  the last query block and the 16-row tiles with the largest page unions);
+  the last query block and the attention tiles with the largest page unions);
 * the ragged 8K+24K+48K+96K batch (per-sequence selection and attention);
 * the whole 32-layer MiniCPM4.1-8B-shaped prefill at 64K (layer-0 stages
   against the oracle, then the full prefill finite and deterministic);
@@ -20,6 +20,7 @@ from gpu_helpers import oracle_select_rows, plan_structure_errors, spread_rows
 from leanselect_amd import minicpm, workloads
 from leanselect_amd.ops import (compress_k, leanselect_prefill_topk_idx, nosa_prefill_topk_idx,
                                 nosa_sparse_attention, sparse_attention)
+from leanselect_amd.ops.attention import attention_tile_rows
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -34,9 +35,11 @@ def _select(case):
     return kc, cu_c, ids
 
 
-def tile_unions(ids: torch.Tensor, cu_host: list[int], tile: int = 16):
-    """(group, first row, distinct pages) of every 16-row tile of each sequence."""
+def tile_unions(ids: torch.Tensor, cu_host: list[int], tile: int | None = None):
+    """(group, first row, distinct pages) of every ``tile``-row tile of each sequence
+    (by default the attention kernel's tile for this plan width)."""
     G, N, T = ids.shape
+    tile = tile or attention_tile_rows(T)
     res = []
     for b in range(len(cu_host) - 1):
         s, e = cu_host[b], cu_host[b + 1]
@@ -54,8 +57,9 @@ def tile_unions(ids: torch.Tensor, cu_host: list[int], tile: int = 16):
     return res
 
 
-def widest_tile_rows(ids, cu_host, count=2, tile=16):
+def widest_tile_rows(ids, cu_host, count=2, tile=None):
     """All rows of the ``count`` tiles with the largest unions (per group)."""
+    tile = tile or attention_tile_rows(ids.shape[-1])
     un = tile_unions(ids, cu_host, tile)
     rows, best = set(), []
     for g in range(ids.shape[0]):

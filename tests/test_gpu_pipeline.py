@@ -10,7 +10,7 @@ import oracle
 from gpu_helpers import oracle_select_rows, plan_structure_errors, spread_rows
 from leanselect_amd import _hip, workloads
 from leanselect_amd.ops import compress_k, leanselect_prefill_topk_idx, sparse_attention
-from leanselect_amd.ops.attention import infllmv2_attn_varlen_func
+from leanselect_amd.ops.attention import attention_tile_rows, infllmv2_attn_varlen_func
 from leanselect_amd.ops.nosa import nosa_sparse_attention
 from leanselect_amd.prefill import leanselect_sparse_prefill
 
@@ -230,9 +230,9 @@ def test_attention_ragged_batch():
 
 
 def test_attention_every_row_of_a_ragged_batch():
-    """Every row of a batch whose tile count (16-row tiles per sequence) is far from a
-    multiple of the launch's rounding: each tile index reaches exactly one workgroup
-    of the XCD-dealt grid, and surplus workgroups exit without writing."""
+    """Every row of a batch whose tile count (24-row tiles per sequence, 64-id plans)
+    is far from a multiple of the launch's rounding: each tile index reaches exactly
+    one workgroup of the XCD-dealt grid, and surplus workgroups exit without writing."""
     case, ids = _attention_case(lens=(700, 1300, 64, 17, 2500, 333), seed=8)
     _check_attention(case, ids, list(range(case.cu_host[-1])))
 
@@ -247,15 +247,41 @@ def test_attention_messy_ids_duplicates_unsorted_out_of_range():
     _check_attention(case, messy.to(DEV), rows)
 
 
+@pytest.mark.parametrize("take,dtype", [(85, torch.bfloat16), (86, torch.bfloat16),
+                                        (128, torch.float16)])
+def test_attention_tile_sizes_at_the_union_cap(take, dtype):
+    """Plans of up to 85 ids a row run 24-row tiles, wider ones 16-row tiles.  Row r of
+    a tile takes pages r*take .. r*take + take - 1 (mod the visible pages), so late in
+    a 131072-token sequence no two rows of a tile share a page and the tiles' unions
+    reach 24 x 85 = 2040 and 16 x 128 = 2048 pages, the size of the kernel's union
+    table; earlier rows repeat ids, which the kernel drops."""
+    N = 131072
+    case = workloads.hidden_space_layer((N,), device=DEV, dtype=dtype, seed=31)
+    G = case.k.shape[1]
+    tile = attention_tile_rows(take)
+    assert tile == (24 if take <= 85 else 16)
+    t = torch.arange(N, dtype=torch.int64)
+    visible = (t // 64 + 1)[:, None]
+    base = (t % tile)[:, None] * take + torch.arange(take, dtype=torch.int64)[None, :]
+    ids = torch.stack([(base + 977 * g) % visible for g in range(G)]).to(torch.int32)
+    last = (N // tile - 1) * tile
+    for g in range(G):
+        assert ids[g, last : last + tile].unique().numel() == tile * take
+    rows = sorted(set(spread_rows(case.cu_host, per_seq=24)) |
+                  set(range(last - tile, last + tile)) | set(range(N - 8, N)))
+    _check_attention(case, ids.to(DEV), rows)
+
+
 def test_attention_union_sizes_with_small_factors():
     """Tiles whose union has 1, 2, 7, 14, 21, 35 or 49 pages (the visit order is a
     stride permutation of the union, which must stay a bijection for every size)."""
     case, ids = _attention_case(lens=(4096,), seed=10)
     G, N, T = ids.shape
+    tile = attention_tile_rows(T)
     crafted = torch.full((G, N, T), -1, dtype=torch.int32)
     sizes = [1, 2, 7, 14, 21, 35, 49]
     for t in range(N):
-        k = sizes[(t // 16) % len(sizes)]
+        k = sizes[(t // tile) % len(sizes)]
         pages = [p for p in range(k) if p <= t // 64][:T]
         crafted[:, t, : len(pages)] = torch.tensor(pages, dtype=torch.int32)
     rows = spread_rows(case.cu_host, per_seq=64)
