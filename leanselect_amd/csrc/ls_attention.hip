@@ -108,7 +108,7 @@ __global__ void ls_attn_status_clear_kernel(int32_t* __restrict__ status) {
 #define LS_ATT_STAGE_BYTES (2 * LS_ATT_KBYTES)  // + V^T page: 128 rows x 128 B
 #define LS_ATT_WORDS (LS_ATTN_MAX_PAGES / 32)
 #ifndef LS_ATT_XCD_CHUNK
-#define LS_ATT_XCD_CHUNK 32                  // consecutive tiles per XCD run
+#define LS_ATT_XCD_CHUNK 16                  // consecutive tiles per XCD run
 #endif
 #ifndef LS_ATT_SHARE_STRIDED
 #define LS_ATT_SHARE_STRIDED 25              // plan ids per union page (x10) for the strided order
