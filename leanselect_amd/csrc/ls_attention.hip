@@ -334,7 +334,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
     m_run[j] = -INFINITY;
     l_run[j] = 0.f;
     thr[j] = -INFINITY;
-    jmax_r[j] = row < n_rows ? (int)row_jmax(row) : -1;
+    // Wave-uniform, so each chunk's row mask below is scalar work.
+    jmax_r[j] = __builtin_amdgcn_readfirstlane(row < n_rows ? (int)row_jmax(row) : -1);
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[j][db] = ls_f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -527,7 +528,6 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       uint32_t need = 0;
 #pragma unroll
       for (int j = 0; j < TPW; ++j) need |= (uint32_t)(((sel >> j) & 1u) && base <= jmax_r[j]) << j;
-      need = __builtin_amdgcn_readfirstlane(need);
       if (!need) continue;
       // The chunk's K and V^T fragments are read once and shared by the rows.
       const int R0 = 32 * c + r, R1 = 32 * c + 16 + r;
@@ -544,7 +544,6 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
 #pragma unroll
         for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
       }
-      const int key0 = base + 8 * q;
       ls_f32x4 cbv0, cbv1;  // this lane's eight key biases (BIAS only)
       if constexpr (BIAS) {
         const float* bp = s_bias + (ui % LS_ATT_STAGES) * 64 + 32 * c + 8 * q;
@@ -565,9 +564,14 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       auto soft_pv = [&](int j, const ls_f32x4& s0, const ls_f32x4& s1) {
         float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
         if (base + 31 > jmax_r[j]) {  // the chunk crosses this row's causal frontier
+          // This lane's last visible key offset, formed here so that the eight
+          // key indices are not kept for every chunk (the empty asm keeps the
+          // compiler from rewriting the compares back into them).
+          int lim = jmax_r[j] - base - 8 * q;
+          asm("" : "+v"(lim));
 #pragma unroll
           for (int i = 0; i < 8; ++i)
-            if (key0 + i > jmax_r[j]) sv[i] = -INFINITY;
+            if (i > lim) sv[i] = -INFINITY;
         }
         // With a bias the scores are taken to base-2 units here (thr, m_run
         // and the maxima below are then all in those units).
