@@ -584,9 +584,10 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
         }
         // Plain maxima: the compiler inserts the wait states an MFMA result
         // needs before a VALU read (it cannot for inline asm), and this file is
-        // built without IEEE NaN quieting, so they fuse into v_max3.
-        const float lmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), sv[2]),
-                                 fmaxf(fmaxf(fmaxf(sv[3], sv[4]), sv[5]), fmaxf(sv[6], sv[7])));
+        // built without IEEE NaN quieting, so they fuse into v_max3 (grouped
+        // here as three v_max3 and one v_max).
+        const float lmax = fmaxf(fmaxf(fmaxf(sv[6], sv[7]), fmaxf(fmaxf(sv[0], sv[1]), sv[2])),
+                                 fmaxf(fmaxf(sv[3], sv[4]), sv[5]));
         // Rescale only when some head's max grows by more than 2^8 (or when the
         // page's V scale leaves too little fp16 headroom for P up to 2^8).
         if (__ballot(lmax > thr[j]) != 0ull || v_e > 7) {
