@@ -272,6 +272,21 @@ def test_attention_tile_sizes_at_the_union_cap(take, dtype):
     _check_attention(case, ids.to(DEV), rows)
 
 
+@pytest.mark.parametrize("take", [0, 5])
+def test_attention_plans_without_pages(take):
+    """Plans with no ids (take 0) or only -1 ids: no union page, so every row's
+    output is zero and its log-sum-exp +inf (flash attention's empty-row rule),
+    and no wait of the ring is entered."""
+    case = workloads.hidden_space_layer((700, 300), device=DEV, seed=12)
+    G, N = case.k.shape[1], case.cu_host[-1]
+    ids = torch.full((G, N, take), -1, dtype=torch.int32, device=DEV)
+    out, lse = sparse_attention(case.q, case.k, case.v, case.cu_seqlens, case.cu_seqlens,
+                                case.max_seqlen, case.max_seqlen, ids, return_lse=True,
+                                sync_status=True)
+    assert bool((out == 0).all())
+    assert bool(torch.isposinf(lse).all())
+
+
 def test_attention_union_sizes_with_small_factors():
     """Tiles whose union has 1, 2, 7, 14, 21, 35 or 49 pages (the visit order is a
     stride permutation of the union, which must stay a bijection for every size)."""
