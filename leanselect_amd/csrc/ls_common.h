@@ -105,6 +105,29 @@ __device__ __forceinline__ float ls_shfl_xor(float v, int mask) {
   return __shfl_xor(v, mask, LS_WAVE);
 }
 
+// Wave-wide maximum / minimum of a 32-bit value, with all 64 lanes active.
+// DPP steps inside each row of 16 lanes (swaps within quads, then the
+// half-row and row mirrors) leave every lane with its row's result; the four
+// row results are then read into scalar registers.  No LDS round trip, unlike
+// a shuffle reduction.  The result is uniform.  (No source lane of these
+// patterns lies outside its row, so bound_ctrl changes nothing here; it lets
+// each move fold into the min/max as one DPP instruction.)
+template <bool MAX>
+__device__ __forceinline__ uint32_t ls_wave_extreme_u32(uint32_t x) {
+  auto pick = [](uint32_t a, uint32_t b) { return MAX ? max(a, b) : min(a, b); };
+  x = pick(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, true));
+  x = pick(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, true));
+  x = pick(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x141, 0xF, 0xF, true));
+  x = pick(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x140, 0xF, 0xF, true));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+  return pick(pick(a, b), pick(c, d));
+}
+__device__ __forceinline__ uint32_t ls_wave_max_u32(uint32_t x) { return ls_wave_extreme_u32<true>(x); }
+__device__ __forceinline__ uint32_t ls_wave_min_u32(uint32_t x) { return ls_wave_extreme_u32<false>(x); }
+
 // NaN-propagating maximum (v_maximum3_f32 on gfx950), as torch's amax and
 // max_pool1d propagate NaN.  Only meaningful where NaN is honoured (files
 // built without -fno-honor-nans).
@@ -186,10 +209,7 @@ __device__ __forceinline__ uint32_t ls_kth_key_row(const uint32_t (&key)[NS], in
     uint32_t sk[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sk[i] = i * 64 + lane < n ? scr[i * 64 + lane] : 0u;
-    uint32_t hi = m1;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, LS_WAVE));
-    hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)hi);
+    const uint32_t hi = ls_wave_max_u32(m1);
     const uint32_t d = lo ^ hi;
     if (d == 0u) return lo;
     const int tb = 31 - __builtin_clz(d);

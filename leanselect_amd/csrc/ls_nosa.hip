@@ -281,10 +281,7 @@ __device__ __forceinline__ int ls_nosa_mark_packed(uint32_t* __restrict__ scr, i
   uint32_t pk[NP];
 #pragma unroll
   for (int i = 0; i < NP; ++i) pk[i] = i * 64 + lane < n ? scr[i * 64 + lane] : 0u;
-  uint32_t hi = m1;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, LS_WAVE));
-  hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)hi);
+  const uint32_t hi = ls_wave_max_u32(m1);
   uint32_t T = lo;
   const uint32_t d = lo ^ hi;
   if (d != 0u) {
@@ -361,9 +358,7 @@ __device__ __forceinline__ int ls_nosa_stage1_finish(uint32_t* __restrict__ scr,
     pk[i] = valid && !forced ? (e | 0x80000000u) : 0u;
     hk = max(hk, pk[i] >> 16);
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) hk = max(hk, (uint32_t)__shfl_xor((int)hk, o, LS_WAVE));
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)hk);
+  const uint32_t hi = ls_wave_max_u32(hk);
   uint32_t T = lo;
   const uint32_t d = lo ^ hi;
   if (d != 0u) {
@@ -442,14 +437,7 @@ __device__ __forceinline__ int ls_nosa_stage1_bf16(const uint16_t* __restrict__ 
   if (__ballot(__builtin_isnan(m1) || m1 == INFINITY) != 0ull) return -1;
   const uint32_t k1 = ls_order_key16((uint16_t)(__float_as_uint(m1) >> 16));
   const uint32_t kb = ls_order_key16((uint16_t)(__float_as_uint(m2) >> 16));
-  uint32_t kmin = kb, kmax = k1;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, LS_WAVE));
-    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, LS_WAVE));
-  }
-  kmin = (uint32_t)__builtin_amdgcn_readfirstlane((int)kmin);
-  kmax = (uint32_t)__builtin_amdgcn_readfirstlane((int)kmax);
+  const uint32_t kmin = ls_wave_min_u32(kb), kmax = ls_wave_max_u32(k1);
   const uint32_t dk = kmin ^ kmax;
   const int top = dk ? 31 - __builtin_clz(dk) : -1;
   uint32_t lo = top >= 0 ? kmin & ~((2u << top) - 1u) : kmin;

@@ -87,21 +87,20 @@ __device__ __forceinline__ uint32_t ls_topk_row(const void* __restrict__ P, int6
 // maxima, reduced here), then the chosen columns written in column order.
 // Returns T (uniform).
 // (or_mask is OR-ed into every gathered entry as it is read back: the bf16
-// fast path below gathers raw score bits, which become order keys that way.)
+// fast path below gathers raw score bits, which become order keys that way;
+// with m1_reduced, m1 is already the row maximum and is not reduced again.)
 template <int NP>
 __device__ __forceinline__ uint32_t ls_topk_emit_packed(const uint32_t* __restrict__ scr, int n,
                                                         uint32_t lo, uint32_t m1, int kk,
                                                         int lo_end, int lane,
                                                         int32_t* __restrict__ orow, int id_max,
                                                         const LsInvalidKeys& rule = LsInvalidKeys(),
-                                                        uint32_t or_mask = 0u) {
+                                                        uint32_t or_mask = 0u,
+                                                        bool m1_reduced = false) {
   uint32_t pk[NP];
 #pragma unroll
   for (int i = 0; i < NP; ++i) pk[i] = i * 64 + lane < n ? (scr[i * 64 + lane] | or_mask) : 0u;
-  uint32_t hi = m1;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, LS_WAVE));
-  hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)hi);
+  const uint32_t hi = m1_reduced ? m1 : ls_wave_max_u32(m1);
   // T: the largest 16-bit key with #{key >= T} >= kk, sharing lo's and hi's
   // common bit prefix.
   uint32_t T = lo;
@@ -325,14 +324,7 @@ __device__ __forceinline__ bool ls_topk_row16_bf16(const uint16_t* __restrict__ 
   // lo: the kk-th largest of the 128 keys, bisected below the bit prefix that
   // all of them share (that of the smallest second and the largest first key),
   // with the loop unrolled.
-  uint32_t kmin = k2, kmax = k1;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, LS_WAVE));
-    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, LS_WAVE));
-  }
-  kmin = (uint32_t)__builtin_amdgcn_readfirstlane((int)kmin);
-  kmax = (uint32_t)__builtin_amdgcn_readfirstlane((int)kmax);
+  const uint32_t kmin = ls_wave_min_u32(k2), kmax = ls_wave_max_u32(k1);
   const uint32_t dk = kmin ^ kmax;
   const int top = dk ? 31 - __builtin_clz(dk) : -1;  // highest differing bit
   uint32_t lo = top >= 0 ? kmin & ~((2u << top) - 1u) : kmin;
@@ -362,11 +354,14 @@ __device__ __forceinline__ bool ls_topk_row16_bf16(const uint16_t* __restrict__ 
   }
   if (n > 256) return false;
   if (n <= 64)
-    T = ls_topk_emit_packed<1>(scr, n, lo, k1, kk, lo_end, lane, orow, id_max, rule, 0x80000000u);
+    T = ls_topk_emit_packed<1>(scr, n, lo, kmax, kk, lo_end, lane, orow, id_max, rule, 0x80000000u,
+                                   true);
   else if (n <= 128)
-    T = ls_topk_emit_packed<2>(scr, n, lo, k1, kk, lo_end, lane, orow, id_max, rule, 0x80000000u);
+    T = ls_topk_emit_packed<2>(scr, n, lo, kmax, kk, lo_end, lane, orow, id_max, rule, 0x80000000u,
+                                   true);
   else
-    T = ls_topk_emit_packed<4>(scr, n, lo, k1, kk, lo_end, lane, orow, id_max, rule, 0x80000000u);
+    T = ls_topk_emit_packed<4>(scr, n, lo, kmax, kk, lo_end, lane, orow, id_max, rule, 0x80000000u,
+                                   true);
   return true;
 }
 
