@@ -6,7 +6,7 @@
 // keys are those of the valid ids in topk_idx[g, t, :] (each page once) with
 // j <= t + len_k - len_q when causal; all H/G heads of the group share the plan.
 //
-// Design (one workgroup per 16 or 24 query rows of one KV group and 16-head tile):
+// Design (one workgroup per 24 query rows of one KV group and 16-head tile):
 //   * the plan row is turned into an ascending, duplicate-free page list with
 //     an LDS bitmap (ids past the causal frontier are dropped);
 //   * S^T = K . Q^T on v_mfma_f32_16x16x32: keys are MFMA rows, the 16 heads of
@@ -89,15 +89,15 @@ __global__ void ls_attn_status_clear_kernel(int32_t* __restrict__ status) {
 // ---------------------------------------------------------------------------
 // Tile kernel: one workgroup = 8 x TPW consecutive query rows of one sequence
 // and one KV group for 16 of its query heads (8 waves x TPW rows, two waves per
-// SIMD; TPW = 3, 24-row tiles, when a row has at most LS_ATT_UNION_CAP / 24
-// ids, else TPW = 2).  The rows' page plans are OR-ed into a union page list;
+// SIMD; the launcher uses TPW = 3, 24-row tiles, for every plan of up to
+// LS_ATTN_MAX_TAKE ids).  The rows' page plans are OR-ed into a union page list;
 // each union page of staged K and V^T is streamed once into a 4-stage LDS ring
 // with direct global->LDS loads, and every row that selected the page runs its
 // MFMAs on it.  Rows that did not select a page skip it (no masked-out work).
 // A wave keeps its rows' O^T accumulators (TPW x 8 x 4 floats per lane) and
 // Q^T fragments in registers.  Larger tiles share each page copy among more
 // rows; three rows of O and Q are what the register file holds at two waves per
-// SIMD (with the V^T fragments read per row instead of shared).
+// SIMD (with each row reading the chunk's V^T fragments where it uses them).
 // ---------------------------------------------------------------------------
 #ifndef LS_ATT_WAVES
 #define LS_ATT_WAVES 8                       // waves per workgroup
@@ -116,14 +116,15 @@ __global__ void ls_attn_status_clear_kernel(int32_t* __restrict__ status) {
 #ifndef LS_ATT_SPIN_SLEEP
 #define LS_ATT_SPIN_SLEEP 1                  // s_sleep units between a waiting wave's polls
 #endif
-#define LS_ATT_UNION_CAP (64 * 32)           // union pages of a tile: one 32-bit need word per lane
+#define LS_ATT_UNION_CAP (64 * 64)           // union pages of a tile: one 64-bit need word per lane
 
 // Tile geometry for TPW rows per wave: rows per tile, the most ids per row it
 // accepts (so that its union fits LS_ATT_UNION_CAP) and the union bound.
 template <int TPW>
 struct LsAttTile {
   static constexpr int kTile = LS_ATT_WAVES * TPW;
-  static constexpr int kMaxTake = TPW == 2 ? LS_ATTN_MAX_TAKE : LS_ATT_UNION_CAP / kTile;
+  static constexpr int kMaxTake =
+      LS_ATTN_MAX_TAKE < LS_ATT_UNION_CAP / kTile ? LS_ATTN_MAX_TAKE : LS_ATT_UNION_CAP / kTile;
   static constexpr int kMaxUnion = kTile * kMaxTake;
   static_assert(kTile <= 32, "row masks are 32-bit");
   static_assert(kMaxUnion <= LS_ATT_UNION_CAP, "one need word per lane");
@@ -245,7 +246,8 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
   constexpr int D = 128;
   constexpr int TILE = LsAttTile<TPW>::kTile;
   constexpr int MAX_UNION = LsAttTile<TPW>::kMaxUnion;
-  constexpr int NEED_WORDS = (MAX_UNION + 31) / 32;  // need-mask words per wave
+  constexpr int NEED_LANES = (MAX_UNION + 63) / 64;  // lanes holding a 64-bit need word
+  constexpr int NEED_WORDS = 2 * NEED_LANES;         // 32-bit need-mask words per wave
   constexpr uint32_t ROWS_MASK = (1u << TPW) - 1u;
   // The per-row page bitmaps are only needed before streaming starts and
   // share their LDS with the ring.
@@ -429,9 +431,12 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
                     // the ring may be written
   LS_WAIT_VMCNT(0);
   // This wave's pages: bit b of lane l is set when one of its rows selected
-  // union page 32 l + b (the union holds at most 64 x 32 pages).
-  static_assert(NEED_WORDS <= 64, "one need word per lane");
-  const uint32_t wneed = lane < NEED_WORDS ? s_wneed[w][lane] : 0u;
+  // union page 64 l + b (the union holds at most 64 x 64 pages).
+  static_assert(NEED_LANES <= 64, "one need word per lane");
+  const uint64_t wneed =
+      lane < NEED_LANES
+          ? ((uint64_t)s_wneed[w][2 * lane + 1] << 32) | (uint64_t)s_wneed[w][2 * lane]
+          : 0ull;
 
   // ---- staging ----
   // One wave copies a whole union page into its stage: the page's staged
@@ -540,10 +545,6 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
       }
       // V^T row 16 db + r (so (row >> 1) & 7 == (r >> 1) & 7), logical chunk 4c + q.
       const uint8_t* vrow = vb + r * 128 + (((4 * c + q) ^ ((r >> 1) & 7)) << 4);
-      if constexpr (TPW == 2) {  // two rows share the chunk's V^T fragments
-#pragma unroll
-        for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
-      }
       ls_f32x4 cbv0, cbv1;  // this lane's eight key biases (BIAS only)
       if constexpr (BIAS) {
         const float* bp = s_bias + (ui % LS_ATT_STAGES) * 64 + 32 * c + 8 * q;
@@ -617,10 +618,9 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
         }
         const float lsum = ls_sum_f16x2(pf[3], ls_sum_f16x2(pf[2], ls_sum_f16x2(pf[1], ls_sum_f16x2(pf[0], 0.f))));
         l_run[j] = fmaf(lsum, p_unscale, l_run[j]);
-        if constexpr (TPW != 2) {  // V^T fragments are read where they are used
+        // The row's V^T fragments, read where they are used.
 #pragma unroll
-          for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
-        }
+        for (int db = 0; db < 8; ++db) vf[db] = *reinterpret_cast<const ls_u32x4*>(vrow + db * 2048);
 #pragma unroll
         for (int db = 0; db < 8; ++db) o[j][db] = LsElem<LS_F16>::mfma(vf[db], pf, o[j][db]);
       };
@@ -636,12 +636,14 @@ __global__ __launch_bounds__(LS_ATT_THREADS, LS_ATT_THREADS / 256) void ls_attn_
 
   // Next page of this wave: the lowest set need bit above `after` (n_union if none).
   auto next_page = [&](int after) -> int {
-    const int from = after + 1, fl = from >> 5;
-    const uint32_t word = lane < fl ? 0u : (lane == fl ? wneed & (0xffffffffu << (from & 31)) : wneed);
-    const uint64_t lanes = __ballot(word != 0u);
+    const int from = after + 1, fl = from >> 6;
+    const uint64_t word = lane < fl ? 0ull : (lane == fl ? wneed & (~0ull << (from & 63)) : wneed);
+    const uint64_t lanes = __ballot(word != 0ull);
     if (lanes == 0ull) return n_union;
     const int L = (int)__builtin_ctzll(lanes);
-    return 32 * L + (int)__builtin_ctz((uint32_t)__builtin_amdgcn_readlane((int)word, L));
+    const uint64_t wl = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(word >> 32), L) << 32) |
+                        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)word, L);
+    return 64 * L + (int)__builtin_ctzll(wl);
   };
   // The next page's union entry is read before the current page is computed.
   int ui = next_page(-1);
@@ -832,9 +834,10 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   float* cb = bias ? (float*)(ws + L.cb) : nullptr;
   int32_t* tok = (int32_t*)(ws + L.tok);
   int32_t* status = status_out ? status_out : (int32_t*)(ws + L.status);
-  // 24-row tiles when every row's ids fit their union bound, else 16-row tiles.
-  const bool tile24 = take <= LsAttTile<3>::kMaxTake;
-  const int tile_rows = tile24 ? LsAttTile<3>::kTile : LsAttTile<2>::kTile;
+  // 24-row tiles (three rows a wave): their union bound holds every plan accepted.
+  constexpr int kTpw = 3;
+  static_assert(LsAttTile<kTpw>::kMaxTake >= LS_ATTN_MAX_TAKE, "every accepted plan fits a tile");
+  const int tile_rows = LsAttTile<kTpw>::kTile;
   hipLaunchKernelGGL(ls_attn_plan_kernel, dim3(1), dim3(64), 0, s, cu_seqlens_q, cu_seqlens_k,
                      batch, tile_rows, pg, tiles, tok, LS_ATT_UNION_CAP + 1, status);
   int rc = ls_check_launch("ls_attn_plan_kernel");
@@ -874,22 +877,12 @@ int attn_run(const char* who, const void* q, int64_t q_row_stride, const void* k
   grid, s, q, q_row_stride, kv, L, vexp, cb, tok, cu_seqlens_q, cu_seqlens_k, pg,              \
       tiles, batch, total_q, num_kv_heads, gs, topk_idx, take, scale_log2, causal, out, lse, \
       status
-  if (tile24) {
-    if (dtype == LS_BF16) {
-      if (bias) launch_tile<LS_BF16, true, 3>(LS_TILE_ARGS);
-      else launch_tile<LS_BF16, false, 3>(LS_TILE_ARGS);
-    } else {
-      if (bias) launch_tile<LS_F16, true, 3>(LS_TILE_ARGS);
-      else launch_tile<LS_F16, false, 3>(LS_TILE_ARGS);
-    }
+  if (dtype == LS_BF16) {
+    if (bias) launch_tile<LS_BF16, true, kTpw>(LS_TILE_ARGS);
+    else launch_tile<LS_BF16, false, kTpw>(LS_TILE_ARGS);
   } else {
-    if (dtype == LS_BF16) {
-      if (bias) launch_tile<LS_BF16, true, 2>(LS_TILE_ARGS);
-      else launch_tile<LS_BF16, false, 2>(LS_TILE_ARGS);
-    } else {
-      if (bias) launch_tile<LS_F16, true, 2>(LS_TILE_ARGS);
-      else launch_tile<LS_F16, false, 2>(LS_TILE_ARGS);
-    }
+    if (bias) launch_tile<LS_F16, true, kTpw>(LS_TILE_ARGS);
+    else launch_tile<LS_F16, false, kTpw>(LS_TILE_ARGS);
   }
 #undef LS_TILE_ARGS
   return ls_check_launch("ls_attn_tile_kernel");

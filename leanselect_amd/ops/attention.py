@@ -12,15 +12,14 @@ from .. import _hip
 
 __all__ = ["attention_tile_rows", "infllmv2_attn_varlen_func", "sparse_attention"]
 
-# Page-union table of one attention workgroup (LS_ATT_UNION_CAP in csrc/ls_attention.hip).
-_UNION_CAP = 2048
-
-
 def attention_tile_rows(take: int) -> int:
     """Query rows per workgroup of the attention kernel for plans of ``take`` ids a
-    row: 24 (three rows per wave) while 24 rows' ids fit the union table, else 16.
-    The launcher in csrc/ls_attention.hip makes the same choice."""
-    return 24 if take <= _UNION_CAP // 24 else 16
+    row: 24 (three rows per wave) for every width it accepts (at most 128 ids; the
+    union of a tile, at most 3072 pages, fits its 4096-entry table), as the launcher
+    in csrc/ls_attention.hip uses."""
+    if take > 128:
+        raise ValueError("the attention kernel accepts at most 128 ids per row")
+    return 24
 
 
 def sparse_attention(

@@ -247,19 +247,19 @@ def test_attention_messy_ids_duplicates_unsorted_out_of_range():
     _check_attention(case, messy.to(DEV), rows)
 
 
-@pytest.mark.parametrize("take,dtype", [(85, torch.bfloat16), (86, torch.bfloat16),
-                                        (128, torch.float16)])
-def test_attention_tile_sizes_at_the_union_cap(take, dtype):
-    """Plans of up to 85 ids a row run 24-row tiles, wider ones 16-row tiles.  Row r of
-    a tile takes pages r*take .. r*take + take - 1 (mod the visible pages), so late in
-    a 131072-token sequence no two rows of a tile share a page and the tiles' unions
-    reach 24 x 85 = 2040 and 16 x 128 = 2048 pages, the size of the kernel's union
-    table; earlier rows repeat ids, which the kernel drops."""
-    N = 131072
+@pytest.mark.parametrize("take,dtype,N", [(85, torch.bfloat16, 131072),
+                                          (96, torch.bfloat16, 147456),
+                                          (128, torch.float16, 196608)])
+def test_attention_tile_unions_at_their_bound(take, dtype, N):
+    """Row r of a 24-row tile takes pages r*take .. r*take + take - 1 (mod the visible
+    pages), so at the end of an N-token sequence no two rows of a tile share a page
+    and the last full tile's union holds 24 x take pages: 2040, 2304 and 3072 (the
+    bound of the 128-id plans the kernel accepts, past the 2048 pages of a 32-bit
+    need word per lane); earlier rows repeat ids, which the kernel drops."""
     case = workloads.hidden_space_layer((N,), device=DEV, dtype=dtype, seed=31)
     G = case.k.shape[1]
     tile = attention_tile_rows(take)
-    assert tile == (24 if take <= 85 else 16)
+    assert tile == 24
     t = torch.arange(N, dtype=torch.int64)
     visible = (t // 64 + 1)[:, None]
     base = (t % tile)[:, None] * take + torch.arange(take, dtype=torch.int64)[None, :]
